@@ -1,0 +1,40 @@
+// g3k_device.h - small device helpers shared by the HIP kernels (gfx950, wave64).
+#ifndef G3K_DEVICE_H
+#define G3K_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace g3k {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror: quad q <-> quad 1-q within 8 lanes
+    v += dpp<0x140>(v);  // row_mirror: half h <-> half 1-h within 16 lanes
+    return v;
+}
+
+// Sum over all 64 lanes; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// v_exp_f32: 2^x, flushes to 0 for very negative x.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// bf16 -> f32 is a 16-bit left shift (gemma3_kernels.h:268-275).
+__device__ __forceinline__ float bf16f(uint32_t b) { return __uint_as_float(b << 16); }
+
+}  // namespace g3k
+
+#endif

@@ -1,0 +1,606 @@
+/*
+ * g3attn.c - C11 host side of libg3attn.so: the entry points of
+ * include/g3attn.h.  Argument checking, error codes, the device context (KV
+ * cache, RoPE tables, workspaces, stream) and launch shapes live here; the
+ * kernels sit behind the thin launcher ABI of csrc/g3k.h.
+ *
+ * Built with gcc -std=c11 against the HIP runtime's C API.
+ */
+#include "g3attn.h"
+
+#include <hip/hip_runtime_api.h>
+#include <limits.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../csrc/g3k.h"
+
+#define G3_OK 0
+#define G3_ERR_INVALID_ARG (-1)
+#define G3_ERR_OUT_OF_MEMORY (-4)
+#define G3_ERR_CONTEXT_OVERFLOW (-8)
+
+#define LOG2E 1.4426950408889634f
+#define D G3K_HEAD_DIM
+
+/* ------------------------------------------------------------------ errors */
+
+static _Thread_local char g_err[512];
+
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+const char *g3attn_last_error(void) { return g_err; }
+
+static int hip_fail(hipError_t e, const char *what) {
+    set_err("%s: %s", what, hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? G3_ERR_OUT_OF_MEMORY : G3_ERR_INVALID_ARG;
+}
+
+#define HIP_TRY(call, what)                          \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+/* ------------------------------------------------------------------ config */
+
+void g3attn_default_config(g3attn_config *c) {
+    c->vocab_size = 262208;
+    c->hidden_size = 2560;
+    c->intermediate_size = 10240;
+    c->num_layers = 34;
+    c->num_heads = 8;
+    c->num_kv_heads = 4;
+    c->head_dim = 256;
+    c->max_context = 8192;
+    c->sliding_window = 1024;
+    c->rmsnorm_eps = 1e-6f;
+    c->rope_theta_local = 10000.0f;
+    c->rope_theta_global = 1000000.0f;
+}
+
+int g3attn_is_global_layer(int layer) { return (layer + 1) % 6 == 0; }
+
+static int check_shape(int n_heads, int n_kv, int head_dim) {
+    if (head_dim != D) {
+        set_err("head_dim %d unsupported (this build: %d)", head_dim, D);
+        return 0;
+    }
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv) {
+        set_err("num_heads %d not a multiple of num_kv_heads %d", n_heads, n_kv);
+        return 0;
+    }
+    const int g = n_heads / n_kv;
+    if (g != 1 && g != 2 && g != 4) {
+        set_err("GQA group %d unsupported (1, 2 or 4)", g);
+        return 0;
+    }
+    return 1;
+}
+
+/* ------------------------------------------------------------------ context */
+
+struct g3attn_ctx {
+    g3attn_config cfg;
+    int max_context, device, group;
+    hipStream_t stream;
+    float *rope_local, *rope_global;
+    float **kc, **vc;
+    int *rows;
+    float *ws_acc, *ws_ml;
+    unsigned *counters;
+    /* staging of the host-pointer decode: q | k | v | q_norm | k_norm, and out */
+    unsigned char *h_in, *d_in;
+    float *h_out, *d_out;
+    size_t in_bytes;
+    /* grow-on-demand device buffers for host-pointer batch calls */
+    void *d_big;
+    size_t d_big_cap;
+    int split_rows; /* 0 = heuristic */
+};
+
+static void ctx_free(g3attn_ctx *c) {
+    if (!c) return;
+    if (c->kc)
+        for (int l = 0; l < c->cfg.num_layers; l++) hipFree(c->kc[l]);
+    if (c->vc)
+        for (int l = 0; l < c->cfg.num_layers; l++) hipFree(c->vc[l]);
+    free(c->kc);
+    free(c->vc);
+    free(c->rows);
+    hipFree(c->rope_local);
+    hipFree(c->rope_global);
+    hipFree(c->ws_acc);
+    hipFree(c->ws_ml);
+    hipFree(c->counters);
+    hipFree(c->d_in);
+    hipFree(c->d_out);
+    hipFree(c->d_big);
+    if (c->h_in) hipHostFree(c->h_in);
+    if (c->h_out) hipHostFree(c->h_out);
+    if (c->stream) hipStreamDestroy(c->stream);
+    free(c);
+}
+
+static int alloc_dev(void **p, size_t bytes, const char *what) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        *p = NULL;
+        set_err("hipMalloc(%zu) for %s: %s", bytes, what, hipGetErrorString(e));
+        return 0;
+    }
+    return 1;
+}
+
+static size_t ws_floats(const g3attn_ctx *c) {
+    return (size_t)c->cfg.num_kv_heads * G3K_MAX_SPLITS * c->group * D;
+}
+
+g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
+                          const float *rope_local, const float *rope_global) {
+    g_err[0] = 0;
+    if (!cfg || !rope_local || !rope_global || max_context <= 0) {
+        set_err("g3attn_create: null argument or max_context <= 0");
+        return NULL;
+    }
+    if (!check_shape(cfg->num_heads, cfg->num_kv_heads, cfg->head_dim)) return NULL;
+    if (cfg->num_layers <= 0 || cfg->num_layers > 4096 || cfg->sliding_window <= 0) {
+        set_err("g3attn_create: num_layers %d / sliding_window %d out of range", cfg->num_layers,
+                cfg->sliding_window);
+        return NULL;
+    }
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0) {
+        set_err("g3attn_create: no HIP device (%s)", hipGetErrorString(e));
+        return NULL;
+    }
+    g3attn_ctx *c = (g3attn_ctx *)calloc(1, sizeof *c);
+    if (!c) {
+        set_err("g3attn_create: out of host memory");
+        return NULL;
+    }
+    c->cfg = *cfg;
+    c->max_context = max_context;
+    c->group = cfg->num_heads / cfg->num_kv_heads;
+    const char *ov = getenv("G3ATTN_SPLIT_ROWS");
+    c->split_rows = ov ? atoi(ov) : 0;
+    if (hipGetDevice(&c->device) != hipSuccess) goto fail_rt;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) goto fail_rt;
+
+    const size_t rope_bytes = (size_t)max_context * D * sizeof(float);
+    if (!alloc_dev((void **)&c->rope_local, rope_bytes, "rope table")) goto fail;
+    if (!alloc_dev((void **)&c->rope_global, rope_bytes, "rope table")) goto fail;
+    if (hipMemcpy(c->rope_local, rope_local, rope_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(c->rope_global, rope_global, rope_bytes, hipMemcpyHostToDevice) != hipSuccess)
+        goto fail_rt;
+
+    const int L = cfg->num_layers;
+    c->kc = (float **)calloc((size_t)L, sizeof(float *));
+    c->vc = (float **)calloc((size_t)L, sizeof(float *));
+    c->rows = (int *)calloc((size_t)L, sizeof(int));
+    if (!c->kc || !c->vc || !c->rows) {
+        set_err("g3attn_create: out of host memory");
+        goto fail;
+    }
+    for (int l = 0; l < L; l++) {
+        c->rows[l] = g3attn_is_global_layer(l) ? max_context : cfg->sliding_window;
+        const size_t bytes = (size_t)cfg->num_kv_heads * c->rows[l] * D * sizeof(float);
+        if (!alloc_dev((void **)&c->kc[l], bytes, "K cache")) goto fail;
+        if (!alloc_dev((void **)&c->vc[l], bytes, "V cache")) goto fail;
+        /* the reference callocs its cache (gemma3_transformer.c:199-200) */
+        if (hipMemset(c->kc[l], 0, bytes) != hipSuccess || hipMemset(c->vc[l], 0, bytes) != hipSuccess)
+            goto fail_rt;
+    }
+    if (!alloc_dev((void **)&c->ws_acc, ws_floats(c) * sizeof(float), "decode workspace")) goto fail;
+    if (!alloc_dev((void **)&c->ws_ml, ws_floats(c) / D * 2 * sizeof(float), "decode workspace")) goto fail;
+    if (!alloc_dev((void **)&c->counters, (size_t)cfg->num_kv_heads * sizeof(unsigned), "counters")) goto fail;
+    if (hipMemset(c->counters, 0, (size_t)cfg->num_kv_heads * sizeof(unsigned)) != hipSuccess) goto fail_rt;
+
+    const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D;
+    c->in_bytes = (qs + 2 * ks) * sizeof(float) + 2 * D * sizeof(uint16_t);
+    if (hipHostMalloc((void **)&c->h_in, c->in_bytes, 0) != hipSuccess) goto fail_rt;
+    if (hipHostMalloc((void **)&c->h_out, qs * sizeof(float), 0) != hipSuccess) goto fail_rt;
+    if (!alloc_dev((void **)&c->d_in, c->in_bytes, "staging")) goto fail;
+    if (!alloc_dev((void **)&c->d_out, qs * sizeof(float), "staging")) goto fail;
+    if (hipDeviceSynchronize() != hipSuccess) goto fail_rt;
+    return c;
+
+fail_rt:
+    set_err("g3attn_create: %s", hipGetErrorString(hipGetLastError()));
+fail:
+    ctx_free(c);
+    return NULL;
+}
+
+void g3attn_destroy(g3attn_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    ctx_free(c);
+}
+
+void g3attn_reset(g3attn_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+}
+
+void *g3attn_stream(g3attn_ctx *c) { return c ? (void *)c->stream : NULL; }
+
+int g3attn_synchronize(g3attn_ctx *c) {
+    if (!c) {
+        set_err("g3attn_synchronize: null context");
+        return G3_ERR_INVALID_ARG;
+    }
+    hipSetDevice(c->device);
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_synchronize");
+    return G3_OK;
+}
+
+static int grow_big(g3attn_ctx *c, size_t bytes) {
+    if (bytes <= c->d_big_cap) return G3_OK;
+    HIP_TRY(hipStreamSynchronize(c->stream), "grow staging");
+    hipFree(c->d_big);
+    c->d_big = NULL;
+    c->d_big_cap = 0;
+    if (!alloc_dev(&c->d_big, bytes, "batch staging")) return G3_ERR_OUT_OF_MEMORY;
+    c->d_big_cap = bytes;
+    return G3_OK;
+}
+
+/* ------------------------------------------------------------------ decode */
+
+/* Split-K shape: about 1024 workgroups over all KV heads, at least 128 rows
+ * per workgroup (two 16-row steps per wave), at most G3K_MAX_SPLITS splits. */
+static void choose_splits(int n_stream, int n_kv, int override_rows, int *rps, int *ns) {
+    if (n_stream <= 0) {
+        *rps = 64;
+        *ns = 1;
+        return;
+    }
+    long r;
+    if (override_rows > 0) {
+        r = override_rows;
+    } else {
+        r = ((long)n_stream * n_kv + 1023) / 1024;
+        if (r < 128) r = 128;
+    }
+    r = (r + 63) / 64 * 64;
+    long s = (n_stream + r - 1) / r;
+    if (s > G3K_MAX_SPLITS) {
+        r = ((long)n_stream + G3K_MAX_SPLITS - 1) / G3K_MAX_SPLITS;
+        r = (r + 63) / 64 * 64;
+        s = (n_stream + r - 1) / r;
+    }
+    *rps = (int)r;
+    *ns = (int)s;
+}
+
+static int check_layer(const g3attn_ctx *c, int layer, const char *fn) {
+    if (!c) {
+        set_err("%s: null context", fn);
+        return 0;
+    }
+    if (layer < 0 || layer >= c->cfg.num_layers) {
+        set_err("%s: layer %d out of range [0, %d)", fn, layer, c->cfg.num_layers);
+        return 0;
+    }
+    return 1;
+}
+
+int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
+                         const float *v, const uint16_t *q_norm, const uint16_t *k_norm,
+                         float *attn_out) {
+    if (!check_layer(c, layer, "g3attn_decode")) return G3_ERR_INVALID_ARG;
+    if (!q || !k || !v || !attn_out || pos < 0) {
+        set_err("g3attn_decode: null buffer or pos < 0");
+        return G3_ERR_INVALID_ARG;
+    }
+    if (pos >= c->max_context) {
+        set_err("g3attn_decode: pos %d >= max_context %d", pos, c->max_context);
+        return G3_ERR_CONTEXT_OVERFLOW;
+    }
+    const int is_global = g3attn_is_global_layer(layer);
+    const int W = c->cfg.sliding_window;
+    /* gemma3_transformer.c:318-340: attention range and cache slot */
+    const int seq_len = is_global ? pos + 1 : (pos < W ? pos + 1 : W);
+    const int slot = is_global ? pos : pos % W;
+
+    g3k_decode_args a;
+    memset(&a, 0, sizeof a);
+    a.q = q;
+    a.k_new = k;
+    a.v_new = v;
+    a.q_norm = (q_norm && k_norm) ? q_norm : NULL;
+    a.k_norm = (q_norm && k_norm) ? k_norm : NULL;
+    a.rope_row = (is_global ? c->rope_global : c->rope_local) + (size_t)pos * D;
+    a.eps = c->cfg.rmsnorm_eps;
+    a.kc = c->kc[layer];
+    a.vc = c->vc[layer];
+    a.row_stride = D;
+    a.head_stride = (long long)c->rows[layer] * D;
+    a.n_stream = seq_len - 1;
+    a.skip = slot;
+    a.new_slot = slot;
+    a.mask = NULL;
+    a.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
+    choose_splits(a.n_stream, c->cfg.num_kv_heads, c->split_rows, &a.rows_per_split, &a.n_splits);
+    a.n_kv_heads = c->cfg.num_kv_heads;
+    a.group = c->group;
+    a.out = attn_out;
+    a.ws_acc = c->ws_acc;
+    a.ws_ml = c->ws_ml;
+    a.counters = c->counters;
+    hipSetDevice(c->device);
+    const int rc = g3k_decode(&a, 1, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_decode launch");
+    return G3_OK;
+}
+
+int g3attn_decode(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
+                  const float *v, const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out) {
+    if (!check_layer(c, layer, "g3attn_decode")) return G3_ERR_INVALID_ARG;
+    if (!q || !k || !v || !attn_out) {
+        set_err("g3attn_decode: null buffer");
+        return G3_ERR_INVALID_ARG;
+    }
+    const size_t qs = (size_t)c->cfg.num_heads * D, ks = (size_t)c->cfg.num_kv_heads * D;
+    hipSetDevice(c->device);
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_decode");
+    unsigned char *h = c->h_in;
+    memcpy(h, q, qs * sizeof(float));
+    memcpy(h + qs * 4, k, ks * sizeof(float));
+    memcpy(h + (qs + ks) * 4, v, ks * sizeof(float));
+    const size_t nb = (qs + 2 * ks) * 4;
+    const int norm = q_norm && k_norm;
+    if (norm) {
+        memcpy(h + nb, q_norm, D * sizeof(uint16_t));
+        memcpy(h + nb + D * 2, k_norm, D * sizeof(uint16_t));
+    }
+    HIP_TRY(hipMemcpyAsync(c->d_in, h, norm ? c->in_bytes : nb, hipMemcpyHostToDevice, c->stream),
+            "g3attn_decode upload");
+    const float *dq = (const float *)c->d_in;
+    int rc = g3attn_decode_device(c, layer, pos, dq, dq + qs, dq + qs + ks,
+                                  norm ? (const uint16_t *)(c->d_in + nb) : NULL,
+                                  norm ? (const uint16_t *)(c->d_in + nb + D * 2) : NULL, c->d_out);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(c->h_out, c->d_out, qs * sizeof(float), hipMemcpyDeviceToHost, c->stream),
+            "g3attn_decode download");
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_decode");
+    memcpy(attn_out, c->h_out, qs * sizeof(float));
+    return G3_OK;
+}
+
+/* ------------------------------------------------------------------ KV cache */
+
+int g3attn_kv_append_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *K,
+                            const float *V, const uint16_t *k_norm) {
+    if (!check_layer(c, layer, "g3attn_kv_append")) return G3_ERR_INVALID_ARG;
+    if (n < 0 || start_pos < 0 || (n > 0 && (!K || !V))) {
+        set_err("g3attn_kv_append: bad arguments");
+        return G3_ERR_INVALID_ARG;
+    }
+    if ((long)start_pos + n > c->max_context) {
+        set_err("g3attn_kv_append: positions up to %ld exceed max_context %d", (long)start_pos + n - 1,
+                c->max_context);
+        return G3_ERR_CONTEXT_OVERFLOW;
+    }
+    if (n == 0) return G3_OK;
+    const int is_global = g3attn_is_global_layer(layer);
+    const int W = c->cfg.sliding_window;
+    const size_t ks = (size_t)c->cfg.num_kv_heads * D;
+    /* On a ring only the last W tokens survive; skip the rest so no two
+     * tokens of one launch race for a slot. */
+    int skip = (!is_global && n > W) ? n - W : 0;
+    g3k_rope_write_args a;
+    memset(&a, 0, sizeof a);
+    a.K = K + (size_t)skip * ks;
+    a.V = V + (size_t)skip * ks;
+    a.q_norm = k_norm;
+    a.k_norm = k_norm;
+    a.rope = is_global ? c->rope_global : c->rope_local;
+    a.eps = c->cfg.rmsnorm_eps;
+    a.n = n - skip;
+    a.start_pos = start_pos + skip;
+    a.n_heads = c->cfg.num_heads;
+    a.n_kv_heads = c->cfg.num_kv_heads;
+    a.k_dst = c->kc[layer];
+    a.v_dst = c->vc[layer];
+    a.dst_head_stride = (long long)c->rows[layer] * D;
+    a.ring = is_global ? 0 : W;
+    a.dst_pos0 = 0;
+    hipSetDevice(c->device);
+    const int rc = g3k_rope_write(&a, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_kv_append launch");
+    return G3_OK;
+}
+
+int g3attn_kv_append(g3attn_ctx *c, int layer, int start_pos, int n, const float *K,
+                     const float *V, const uint16_t *k_norm) {
+    if (!check_layer(c, layer, "g3attn_kv_append")) return G3_ERR_INVALID_ARG;
+    if (n <= 0) return n == 0 ? G3_OK : G3_ERR_INVALID_ARG;
+    if (!K || !V) {
+        set_err("g3attn_kv_append: null buffer");
+        return G3_ERR_INVALID_ARG;
+    }
+    const size_t kb = (size_t)n * c->cfg.num_kv_heads * D * sizeof(float);
+    hipSetDevice(c->device);
+    int rc = grow_big(c, 2 * kb + 2 * D);
+    if (rc) return rc;
+    unsigned char *b = (unsigned char *)c->d_big;
+    HIP_TRY(hipMemcpyAsync(b, K, kb, hipMemcpyHostToDevice, c->stream), "kv_append upload");
+    HIP_TRY(hipMemcpyAsync(b + kb, V, kb, hipMemcpyHostToDevice, c->stream), "kv_append upload");
+    if (k_norm)
+        HIP_TRY(hipMemcpyAsync(b + 2 * kb, k_norm, D * 2, hipMemcpyHostToDevice, c->stream),
+                "kv_append upload");
+    rc = g3attn_kv_append_device(c, layer, start_pos, n, (const float *)b, (const float *)(b + kb),
+                                 k_norm ? (const uint16_t *)(b + 2 * kb) : NULL);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_kv_append");
+    return G3_OK;
+}
+
+static int kv_copy(g3attn_ctx *c, int layer, int slot, int n, float *k_rows, float *v_rows,
+                   int to_device, const char *fn) {
+    if (!check_layer(c, layer, fn)) return G3_ERR_INVALID_ARG;
+    if (slot < 0 || n < 0 || (long)slot + n > c->rows[layer] || (n > 0 && (!k_rows || !v_rows))) {
+        set_err("%s: rows [%d, %ld) outside the layer's %d cache rows", fn, slot, (long)slot + n,
+                c->rows[layer]);
+        return G3_ERR_INVALID_ARG;
+    }
+    if (n == 0) return G3_OK;
+    const int H = c->cfg.num_kv_heads;
+    const size_t hs = (size_t)c->rows[layer] * D;
+    hipSetDevice(c->device);
+    for (int h = 0; h < H; h++) {
+        float *dk = c->kc[layer] + h * hs + (size_t)slot * D;
+        float *dv = c->vc[layer] + h * hs + (size_t)slot * D;
+        const size_t row = D * sizeof(float), pitch = (size_t)H * row;
+        if (to_device) {
+            HIP_TRY(hipMemcpy2DAsync(dk, row, k_rows + (size_t)h * D, pitch, row, n,
+                                     hipMemcpyHostToDevice, c->stream), fn);
+            HIP_TRY(hipMemcpy2DAsync(dv, row, v_rows + (size_t)h * D, pitch, row, n,
+                                     hipMemcpyHostToDevice, c->stream), fn);
+        } else {
+            HIP_TRY(hipMemcpy2DAsync(k_rows + (size_t)h * D, pitch, dk, row, row, n,
+                                     hipMemcpyDeviceToHost, c->stream), fn);
+            HIP_TRY(hipMemcpy2DAsync(v_rows + (size_t)h * D, pitch, dv, row, row, n,
+                                     hipMemcpyDeviceToHost, c->stream), fn);
+        }
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream), fn);
+    return G3_OK;
+}
+
+int g3attn_kv_write(g3attn_ctx *c, int layer, int slot, int n, const float *k_rows,
+                    const float *v_rows) {
+    return kv_copy(c, layer, slot, n, (float *)k_rows, (float *)v_rows, 1, "g3attn_kv_write");
+}
+
+int g3attn_kv_read(g3attn_ctx *c, int layer, int slot, int n, float *k_rows, float *v_rows) {
+    return kv_copy(c, layer, slot, n, k_rows, v_rows, 0, "g3attn_kv_read");
+}
+
+/* ------------------------------------------------------------------ prefill */
+
+int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
+                          const float *K, const float *V, const uint16_t *q_norm,
+                          const uint16_t *k_norm, float *attn_out) {
+    (void)start_pos; (void)n; (void)Q; (void)K; (void)V; (void)q_norm; (void)k_norm; (void)attn_out;
+    if (!check_layer(c, layer, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
+    set_err("g3attn_prefill: not available in this build");
+    return G3_ERR_INVALID_ARG;
+}
+
+int g3attn_prefill(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
+                   const float *K, const float *V, const uint16_t *q_norm,
+                   const uint16_t *k_norm, float *attn_out) {
+    return g3attn_prefill_device(c, layer, start_pos, n, Q, K, V, q_norm, k_norm, attn_out);
+}
+
+/* ------------------------------------------------------------------ gemma3_gqa */
+
+/* Process-wide state of the gemma3_gqa-shaped entry point. */
+static struct {
+    pthread_mutex_t lock;
+    int ready, device;
+    hipStream_t stream;
+    void *buf;
+    size_t cap;
+    float *ws_acc, *ws_ml;
+    unsigned *counters;
+} g_gqa = {PTHREAD_MUTEX_INITIALIZER, 0, 0, NULL, NULL, 0, NULL, NULL, NULL};
+
+#define GQA_MAX_KV 64
+
+static int gqa_init(void) {
+    if (g_gqa.ready) return G3_OK;
+    HIP_TRY(hipGetDevice(&g_gqa.device), "g3attn_gqa init");
+    HIP_TRY(hipStreamCreateWithFlags(&g_gqa.stream, hipStreamNonBlocking), "g3attn_gqa init");
+    const size_t wsf = (size_t)GQA_MAX_KV * G3K_MAX_SPLITS * 4 * D;
+    if (!alloc_dev((void **)&g_gqa.ws_acc, wsf * sizeof(float), "gqa workspace") ||
+        !alloc_dev((void **)&g_gqa.ws_ml, wsf / D * 2 * sizeof(float), "gqa workspace") ||
+        !alloc_dev((void **)&g_gqa.counters, GQA_MAX_KV * sizeof(unsigned), "gqa counters"))
+        return G3_ERR_OUT_OF_MEMORY;
+    HIP_TRY(hipMemset(g_gqa.counters, 0, GQA_MAX_KV * sizeof(unsigned)), "g3attn_gqa init");
+    g_gqa.ready = 1;
+    return G3_OK;
+}
+
+static int gqa_run(float *output, const float *q, const float *k_cache, const float *v_cache,
+                   int n_heads, int n_kv, int seq_len, int head_dim, float scale, const float *mask) {
+    if (!output || !q || !k_cache || !v_cache || seq_len <= 0) {
+        set_err("g3attn_gqa: null buffer or seq_len <= 0");
+        return G3_ERR_INVALID_ARG;
+    }
+    if (!check_shape(n_heads, n_kv, head_dim)) return G3_ERR_INVALID_ARG;
+    if (n_kv > GQA_MAX_KV) {
+        set_err("g3attn_gqa: n_kv_heads %d > %d", n_kv, GQA_MAX_KV);
+        return G3_ERR_INVALID_ARG;
+    }
+    int rc = gqa_init();
+    if (rc) return rc;
+    hipSetDevice(g_gqa.device);
+    const size_t qs = (size_t)n_heads * D, kvb = (size_t)seq_len * n_kv * D * sizeof(float);
+    const size_t need = qs * 4 * 2 + 2 * kvb + (size_t)seq_len * 4 + 256;
+    if (need > g_gqa.cap) {
+        hipFree(g_gqa.buf);
+        g_gqa.buf = NULL;
+        g_gqa.cap = 0;
+        if (!alloc_dev(&g_gqa.buf, need, "gqa buffers")) return G3_ERR_OUT_OF_MEMORY;
+        g_gqa.cap = need;
+    }
+    unsigned char *b = (unsigned char *)g_gqa.buf;
+    float *dq = (float *)b, *dout = (float *)(b + qs * 4);
+    float *dk = (float *)(b + qs * 8), *dv = (float *)(b + qs * 8 + kvb);
+    float *dm = mask ? (float *)(b + qs * 8 + 2 * kvb) : NULL;
+    hipStream_t s = g_gqa.stream;
+    HIP_TRY(hipMemcpyAsync(dq, q, qs * 4, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
+    HIP_TRY(hipMemcpyAsync(dk, k_cache, kvb, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
+    HIP_TRY(hipMemcpyAsync(dv, v_cache, kvb, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
+    if (mask) HIP_TRY(hipMemcpyAsync(dm, mask, (size_t)seq_len * 4, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
+    g3k_decode_args a;
+    memset(&a, 0, sizeof a);
+    a.q = dq;
+    a.kc = dk;
+    a.vc = dv;
+    a.row_stride = (long long)n_kv * D;
+    a.head_stride = D;
+    a.n_stream = seq_len;
+    a.skip = INT_MAX;
+    a.new_slot = -1;
+    a.mask = dm;
+    a.qscale = scale * LOG2E;
+    choose_splits(seq_len, n_kv, 0, &a.rows_per_split, &a.n_splits);
+    a.n_kv_heads = n_kv;
+    a.group = n_heads / n_kv;
+    a.out = dout;
+    a.ws_acc = g_gqa.ws_acc;
+    a.ws_ml = g_gqa.ws_ml;
+    a.counters = g_gqa.counters;
+    rc = g3k_decode(&a, 0, s);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa launch");
+    HIP_TRY(hipMemcpyAsync(output, dout, qs * 4, hipMemcpyDeviceToHost, s), "g3attn_gqa download");
+    HIP_TRY(hipStreamSynchronize(s), "g3attn_gqa");
+    return G3_OK;
+}
+
+void g3attn_gqa(float *output, const float *q, const float *k_cache, const float *v_cache,
+                int n_heads, int n_kv_heads, int seq_len, int head_dim, float scale,
+                const float *mask, float *scores_buf) {
+    (void)scores_buf;
+    g_err[0] = 0;
+    pthread_mutex_lock(&g_gqa.lock);
+    gqa_run(output, q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim, scale, mask);
+    pthread_mutex_unlock(&g_gqa.lock);
+}

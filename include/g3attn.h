@@ -1,0 +1,158 @@
+/*
+ * g3attn.h - MI355X (gfx950) attention path for gemma3.c, as a C-ABI library
+ * (libg3attn.so).  Plain C types only; every pointer is a caller-owned buffer.
+ *
+ * The library owns a GPU-resident fp32 KV cache per layer and runs the
+ * attention block that follows the Q/K/V projections: per-head QK-RMSNorm,
+ * RoPE from the caller's precomputed table, the KV-cache write and GQA
+ * attention (decode: one token; prefill: a causal / sliding-window batch).
+ * The surrounding engine (loader, tokenizer, GEMVs, sampler) is untouched; a
+ * transformer built with -DUSE_HIP calls these entry points where the
+ * reference runs its CPU attention (hooks: INTEGRATION.md).
+ *
+ * Conventions kept from the reference:
+ *   - 0 on success, a negative gemma3_error code on failure (gemma3.h:57-67):
+ *     -1 invalid argument or GPU runtime error, -4 device allocation failed,
+ *     -8 position >= max_context.  The message is thread-local
+ *     (g3attn_last_error), as gemma3.c:30-41 keeps it.
+ *   - create returns NULL on failure so the caller keeps its CPU path
+ *     (gemma3_transformer.c:889-905 does this for Metal).
+ *   - Not re-entrant per context: one host thread drives a context, as the
+ *     reference drives its transformer (gemma3_transformer.c:38-49).
+ *
+ * Entry points ending in _device take device pointers, enqueue on the
+ * context's stream and return without waiting; all others take host
+ * pointers and return when the result is in the caller's buffer.
+ */
+#ifndef G3ATTN_H
+#define G3ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Field-for-field the layout of gemma3_config (gemma3.h:82-95), so a caller
+ * may pass (const g3attn_config *)&its_gemma3_config.  The attention path
+ * reads num_layers, num_heads, num_kv_heads, head_dim, sliding_window,
+ * rmsnorm_eps; supported: head_dim 256, num_heads / num_kv_heads in {1, 2, 4}. */
+typedef struct {
+    int vocab_size;
+    int hidden_size;
+    int intermediate_size;
+    int num_layers;
+    int num_heads;
+    int num_kv_heads;
+    int head_dim;
+    int max_context;
+    int sliding_window;
+    float rmsnorm_eps;
+    float rope_theta_local;
+    float rope_theta_global;
+} g3attn_config;
+
+typedef struct g3attn_ctx g3attn_ctx;
+
+/* Gemma 3 4B defaults (gemma3.h:36-51; gemma3.c:94-109). */
+void g3attn_default_config(g3attn_config *cfg);
+
+/* 1 if layer `layer` uses global attention: (layer + 1) % 6 == 0
+ * (gemma3_is_global_layer, gemma3.h:347-350). */
+int g3attn_is_global_layer(int layer);
+
+/* RoPE table [max_pos][head_dim/2][cos, sin] with the reference expression
+ * (gemma3_rope_precompute, gemma3_kernels.c:455-468), computed on the host in
+ * fp32 with libm so the GPU sees bit-identical angles. */
+void g3attn_rope_precompute(float *freqs, int max_pos, int head_dim, float theta);
+
+/* Allocates the device KV cache for every layer (gemma3_kv_cache_alloc,
+ * gemma3_transformer.c:180-214: max_context rows on global layers, a
+ * sliding_window ring on local ones) and uploads both RoPE tables
+ * ([max_context][head_dim/2][2], from gemma3_transformer.c:870-883; the Metal
+ * backend uploads them the same way, gemma3_metal.m:603-614).  Replaces
+ * gemma3_metal_init + gemma3_metal_upload_rope (gemma3_metal.h:26, 37-39).
+ * Returns NULL on failure (message in g3attn_last_error). */
+g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
+                          const float *rope_local, const float *rope_global);
+
+/* gemma3_kv_cache_free (gemma3_transformer.c:216-223) + gemma3_metal_free. */
+void g3attn_destroy(g3attn_ctx *ctx);
+
+/* gemma3_kv_cache_reset (gemma3_transformer.c:225-233): positions only.
+ * The cache holds no position state (the caller passes pos), so this waits
+ * for queued work and leaves the rows as they are, like the reference. */
+void g3attn_reset(g3attn_ctx *ctx);
+
+/* One decode step of one layer: the attention section of layer_attention
+ * (gemma3_transformer.c:294-352).  q [num_heads*256], k, v [num_kv_heads*256]
+ * are the raw projections (pre-norm); q_norm / k_norm are the layer's bf16
+ * QK-norm weights [256] (both NULL: no norm, as :295).  Normalises + RoPEs q
+ * and k at pos, writes k, v to slot pos (global) or pos % sliding_window
+ * (local), attends over pos+1 (global) or min(pos+1, window) (local) cached
+ * rows, and writes attn_out [num_heads*256].  Blocking. */
+int g3attn_decode(g3attn_ctx *ctx, int layer, int pos,
+                  const float *q, const float *k, const float *v,
+                  const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out);
+
+/* Prefill of n tokens at positions start_pos..start_pos+n-1 of one layer: the
+ * per-token attention loop of gemma3_transformer_prefill_batched
+ * (gemma3_transformer.c:641-692), batched.  Q [n][num_heads*256],
+ * K, V [n][num_kv_heads*256] (pre-norm), attn_out [n][num_heads*256].
+ * Token i sees exactly the keys the sequential loop gives it: positions
+ * [0, pos] (global) or [pos-window+1, pos] (local), including keys cached by
+ * earlier calls when start_pos > 0.  Blocking. */
+int g3attn_prefill(g3attn_ctx *ctx, int layer, int start_pos, int n,
+                   const float *Q, const float *K, const float *V,
+                   const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out);
+
+/* Device-pointer forms of decode / prefill (same arguments, device memory),
+ * enqueued on the context stream.  For callers whose projections already
+ * live on the GPU, and for timing with inputs resident in HBM. */
+int g3attn_decode_device(g3attn_ctx *ctx, int layer, int pos,
+                         const float *q, const float *k, const float *v,
+                         const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out);
+int g3attn_prefill_device(g3attn_ctx *ctx, int layer, int start_pos, int n,
+                          const float *Q, const float *K, const float *V,
+                          const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out);
+
+/* K-norm + RoPE + cache_kv for n tokens without attention: the key/value half
+ * of the prefill loop (gemma3_transformer.c:650-671).  K, V [n][num_kv_heads*256]
+ * pre-norm (host / device pointers respectively). */
+int g3attn_kv_append(g3attn_ctx *ctx, int layer, int start_pos, int n,
+                     const float *K, const float *V, const uint16_t *k_norm);
+int g3attn_kv_append_device(g3attn_ctx *ctx, int layer, int start_pos, int n,
+                            const float *K, const float *V, const uint16_t *k_norm);
+
+/* Raw access to cache rows (layer_kv_cache.k / .v, gemma3_transformer.c:77-81):
+ * rows slot..slot+n-1 in the reference layout [n][num_kv_heads][256], already
+ * normalised and rotated.  Host pointers; blocking. */
+int g3attn_kv_write(g3attn_ctx *ctx, int layer, int slot, int n,
+                    const float *k_rows, const float *v_rows);
+int g3attn_kv_read(g3attn_ctx *ctx, int layer, int slot, int n,
+                   float *k_rows, float *v_rows);
+
+/* Same signature and semantics as gemma3_gqa (gemma3_kernels.h:188-191,
+ * gemma3_kernels.c:527-597): q [n_heads][head_dim] (final), k_cache / v_cache
+ * [seq_len][n_kv_heads][head_dim], optional additive mask [seq_len];
+ * scores_buf is accepted and unused.  Host pointers, runs on the default
+ * device through a process-wide context; for unit parity and for drop-in use
+ * where no cache-owning context exists.  Failures leave output untouched
+ * and set g3attn_last_error (the reference also returns silently). */
+void g3attn_gqa(float *output, const float *q, const float *k_cache, const float *v_cache,
+                int n_heads, int n_kv_heads, int seq_len, int head_dim,
+                float scale, const float *mask, float *scores_buf);
+
+/* The context's HIP stream (hipStream_t), for callers that interleave their
+ * own work; and a wait for everything queued on it. */
+void *g3attn_stream(g3attn_ctx *ctx);
+int g3attn_synchronize(g3attn_ctx *ctx);
+
+/* Thread-local message of the last failure on this thread ("" if none). */
+const char *g3attn_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G3ATTN_H */

@@ -1,0 +1,159 @@
+/*
+ * ref_harness.c - drives the REAL reference attention code, compiled in place
+ * from /root/reference (never copied), to write golden vectors and to time
+ * the reference CPU baseline.  TEST INFRASTRUCTURE; built into oracle/_ref/
+ * by oracle/Makefile only where /root/reference exists.
+ *
+ * gemma3_transformer.c is #included so that its static functions
+ * layer_attention (gemma3_transformer.c:258-356) and cache_kv (:236-251) are
+ * callable here.  layer_attention begins with the Q/K/V GEMVs and ends with
+ * the o_proj GEMV; the harness feeds it one-hot bf16 projection matrices
+ * with hidden_size = H_q*d + 2*H_kv*d, so x = [q | k | v] maps to q, k, v
+ * exactly (each output is 1.0 * x_j plus exact zeros) and the o_proj output's
+ * first H_q*d entries are attn_out exactly.  Everything between the GEMVs is
+ * the reference's own code.
+ *
+ * The reference's batched prefill loop (gemma3_transformer.c:641-692) sits
+ * inside a USE_BLAS-only function that cannot compile without cblas.h, so
+ * ref_prefill_loop restates only its loop skeleton and calls the
+ * reference's own rmsnorm / rope / cache_kv / causal_mask / gqa.
+ */
+#include "gemma3_transformer.c"
+
+#include <stdint.h>
+
+#define RH_D 256
+
+static uint16_t *g_wq, *g_wk, *g_wv, *g_wo;
+static int g_hq = -1, g_hkv = -1;
+
+static int ensure_weights(int hq, int hkv) {
+    if (g_wq && hq == g_hq && hkv == g_hkv) return 0;
+    free(g_wq); free(g_wk); free(g_wv); free(g_wo);
+    const int qs = hq * RH_D, ks = hkv * RH_D, hs = qs + 2 * ks;
+    g_wq = (uint16_t *)calloc((size_t)qs * hs, 2);
+    g_wk = (uint16_t *)calloc((size_t)ks * hs, 2);
+    g_wv = (uint16_t *)calloc((size_t)ks * hs, 2);
+    g_wo = (uint16_t *)calloc((size_t)hs * qs, 2);
+    if (!g_wq || !g_wk || !g_wv || !g_wo) return -4;
+    const uint16_t one = 0x3F80; /* bf16 1.0 */
+    for (int r = 0; r < qs; r++) g_wq[(size_t)r * hs + r] = one;
+    for (int r = 0; r < ks; r++) g_wk[(size_t)r * hs + qs + r] = one;
+    for (int r = 0; r < ks; r++) g_wv[(size_t)r * hs + qs + ks + r] = one;
+    for (int r = 0; r < qs; r++) g_wo[(size_t)r * qs + r] = one;
+    g_hq = hq;
+    g_hkv = hkv;
+    return 0;
+}
+
+static gemma3_config harness_cfg(int hq, int hkv, int max_context, int window) {
+    gemma3_config c;
+    memset(&c, 0, sizeof c);
+    c.vocab_size = GEMMA3_VOCAB_SIZE;
+    c.num_layers = GEMMA3_NUM_LAYERS;
+    c.num_heads = hq;
+    c.num_kv_heads = hkv;
+    c.head_dim = RH_D;
+    c.hidden_size = hq * RH_D + 2 * hkv * RH_D;
+    c.intermediate_size = GEMMA3_INTERMEDIATE_SIZE;
+    c.max_context = max_context;
+    c.sliding_window = window;
+    c.rmsnorm_eps = GEMMA3_RMSNORM_EPS;
+    c.rope_theta_local = GEMMA3_ROPE_THETA_LOCAL;
+    c.rope_theta_global = GEMMA3_ROPE_THETA_GLOBAL;
+    return c;
+}
+
+/* Thin exports of the reference kernels on the path. */
+void ref_rope_precompute(float *f, int max_pos, int d, float theta) { gemma3_rope_precompute(f, max_pos, d, theta); }
+void ref_rope_apply(float *x, const float *f, int d, int pos) { gemma3_rope_apply_precomputed(x, f, d, pos); }
+void ref_rmsnorm_bf16(float *y, const float *x, const uint16_t *w, int n, float eps) { gemma3_rmsnorm_bf16(y, x, w, n, eps); }
+void ref_softmax(float *x, int n) { gemma3_softmax_inplace(x, n); }
+void ref_causal_mask(float *m, int n, int qp) { gemma3_causal_mask(m, n, qp); }
+void ref_gqa(float *out, const float *q, const float *k, const float *v, int hq, int hkv,
+             int seq_len, int d, float scale, const float *mask, float *scores) {
+    gemma3_gqa(out, q, k, v, hq, hkv, seq_len, d, scale, mask, scores);
+}
+int ref_is_global_layer(int l) { return gemma3_is_global_layer(l); }
+
+/* One decode step through the reference's layer_attention.
+ * q/k/v: pre-norm inputs (not modified).  k_cache/v_cache: the layer's cache,
+ * [rows][hkv][256] (rows = max_context for global layers, window for local).
+ * On return attn_out [hq*256] holds the attention output, q_rot/k_rot (optional)
+ * the normed + RoPE'd q and k, and the cache holds the new row. */
+int ref_layer_decode(float *attn_out, float *q_rot, float *k_rot,
+                     const float *q, const float *k, const float *v,
+                     const uint16_t *q_norm, const uint16_t *k_norm,
+                     float *k_cache, float *v_cache, const float *rope,
+                     int hq, int hkv, int layer, int pos, int max_context, int window) {
+    if (ensure_weights(hq, hkv)) return -4;
+    gemma3_config cfg = harness_cfg(hq, hkv, max_context, window);
+    const int qs = hq * RH_D, ks = hkv * RH_D, hs = cfg.hidden_size;
+    const int cap = max_context > window ? max_context : window;
+    float *x = (float *)malloc((size_t)hs * 4), *out = (float *)malloc((size_t)hs * 4);
+    float *qb = (float *)malloc((size_t)qs * 4), *kb = (float *)malloc((size_t)ks * 4);
+    float *vb = (float *)malloc((size_t)ks * 4), *ab = (float *)malloc((size_t)qs * 4);
+    float *mask = (float *)malloc((size_t)cap * 4), *scores = (float *)malloc((size_t)cap * 4);
+    float *tmp = (float *)malloc((size_t)hs * 4);
+    int rc = 0;
+    if (!x || !out || !qb || !kb || !vb || !ab || !mask || !scores || !tmp) { rc = -4; goto done; }
+    memcpy(x, q, (size_t)qs * 4);
+    memcpy(x + qs, k, (size_t)ks * 4);
+    memcpy(x + qs + ks, v, (size_t)ks * 4);
+    layer_kv_cache cache;
+    cache.k = k_cache;
+    cache.v = v_cache;
+    cache.pos = pos;
+    layer_attention(out, x, g_wq, g_wk, g_wv, g_wo, q_norm, k_norm, &cache, qb, kb, vb, ab,
+                    mask, scores, tmp, rope, NULL, &cfg, layer, pos);
+    memcpy(attn_out, out, (size_t)qs * 4);
+    if (q_rot) memcpy(q_rot, qb, (size_t)qs * 4);
+    if (k_rot) memcpy(k_rot, kb, (size_t)ks * 4);
+done:
+    free(x); free(out); free(qb); free(kb); free(vb); free(ab); free(mask); free(scores); free(tmp);
+    return rc;
+}
+
+/* The per-token prefill attention loop of gemma3_transformer.c:641-692, on the
+ * reference's own functions.  Q, K are modified in place (normed + RoPE'd). */
+int ref_prefill_loop(float *attn_out, float *Q, float *K, const float *V,
+                     const uint16_t *q_norm, const uint16_t *k_norm,
+                     float *k_cache, float *v_cache, const float *rope,
+                     int hq, int hkv, int layer, int start_pos, int n, int max_context, int window) {
+    gemma3_config cfg = harness_cfg(hq, hkv, max_context, window);
+    const int qs = hq * RH_D, ks = hkv * RH_D, d = RH_D;
+    const int cap = max_context > window ? max_context : window;
+    float *mask = (float *)malloc((size_t)cap * 4), *scores = (float *)malloc((size_t)cap * 4);
+    if (!mask || !scores) { free(mask); free(scores); return -4; }
+    layer_kv_cache cache;
+    cache.k = k_cache;
+    cache.v = v_cache;
+    cache.pos = start_pos;
+    const int is_global = gemma3_is_global_layer(layer);
+    const float scale = 1.0f / sqrtf((float)d);
+    for (int i = 0; i < n; i++) {
+        const int pos = start_pos + i;
+        float *qi = Q + (size_t)i * qs, *ki = K + (size_t)i * ks;
+        const float *vi = V + (size_t)i * ks;
+        if (q_norm && k_norm) {
+            for (int h = 0; h < hq; h++) gemma3_rmsnorm_bf16(qi + h * d, qi + h * d, q_norm, d, cfg.rmsnorm_eps);
+            for (int h = 0; h < hkv; h++) gemma3_rmsnorm_bf16(ki + h * d, ki + h * d, k_norm, d, cfg.rmsnorm_eps);
+        }
+        for (int h = 0; h < hq; h++) gemma3_rope_apply_precomputed(qi + h * d, rope, d, pos);
+        for (int h = 0; h < hkv; h++) gemma3_rope_apply_precomputed(ki + h * d, rope, d, pos);
+        cache_kv(&cache, ki, vi, ks, is_global, cfg.sliding_window, pos);
+        int seq_len;
+        if (is_global) {
+            seq_len = pos + 1;
+            gemma3_causal_mask(mask, seq_len, pos);
+        } else {
+            seq_len = (pos < cfg.sliding_window) ? pos + 1 : cfg.sliding_window;
+            for (int s = 0; s < seq_len; s++) mask[s] = 0.0f;
+        }
+        gemma3_gqa(attn_out + (size_t)i * qs, qi, k_cache, v_cache, hq, hkv, seq_len, d, scale,
+                   mask, scores);
+    }
+    free(mask);
+    free(scores);
+    return 0;
+}

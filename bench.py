@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Benchmark of the gemma3.c attention path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME,...]
+
+Headline (the JSON line's `value`): configs[1] of BASELINE.json, global-layer
+decode attention at pos 8191 (L = 8192), whole-job HBM GB/s with every input
+resident in HBM: one step = one g3attn_decode_device call (QK-norm + RoPE +
+cache write + split-K attention + combine, one kernel launch).  Steps rotate
+over 10 distinct 64 MiB caches (two 34-layer contexts x 5 global layers,
+640 MiB) so the 256 MB Infinity Cache cannot serve them.
+
+Algorithmic bytes per decode call = fp32 K + V rows read (8192 B per
+position, 4 KV heads x 256 x 4 B x 2) + q in + out = 8192*L + 16384.
+
+`roofline` is for the decode kernel at the headline config: achieved =
+algorithmic bytes / average kernel duration, the duration from paired HIP
+events around every launch on the library's own stream.
+
+Further configs (reported under "extra", not the headline): configs[0] local
+decode L=512, 128K global-layer decode, the 34-layer decode stack at
+pos 131071 (reference 29 local / 5 global pattern and the config's literal
+28 / 6), and prefill when the library has it.
+
+`cpu_baseline`: the reference's own attention code (oracle/_ref, compiled
+from the reference sources with its fast-mode flags, no BLAS) timed on one
+host core for the headline workload: median of 20 decode steps.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+METRIC = "decode attn µs/token + HBM GB/s at 8K/128K ctx; prefill attn TFLOP/s at 8K"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2516.6
+D, HQ, HKV = 256, 8, 4
+QS, KS = HQ * D, HKV * D
+
+
+def decode_bytes(L: int) -> int:
+    return 8192 * L + 16384
+
+
+def load_binding():
+    spec = importlib.util.spec_from_file_location("g3attn", os.path.join(REPO, "gemma3.c_amd", "g3attn.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["g3attn"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self, G, torch):
+        self.G, self.torch = G, torch
+        self.dev = torch.device("cuda", 0)
+        self.gen = torch.Generator(device=self.dev)
+        self.gen.manual_seed(0x5EED0000)
+
+    def randn_bf16(self, *shape):
+        """Seeded N(0,1) rounded to bf16 (RNE), held as fp32 in HBM."""
+        t = self.torch.randn(*shape, generator=self.gen, device=self.dev, dtype=self.torch.float32)
+        return t.to(self.torch.bfloat16).to(self.torch.float32)
+
+    def context(self, max_context, num_layers=34):
+        G = self.G
+        cfg = G.default_config(max_context=max_context, num_layers=num_layers)
+        return G.Context(cfg, max_context)
+
+    def fill_layer(self, ctx, layer, n_tokens, chunk=16384):
+        """Cache rows 0..n-1 of one layer: seeded K (normed + RoPE'd on the GPU
+        through g3attn_kv_append_device) and V."""
+        zn = self.torch.zeros(D, dtype=self.torch.int16, device=self.dev)
+        for s in range(0, n_tokens, chunk):
+            n = min(chunk, n_tokens - s)
+            K = self.randn_bf16(n, KS)
+            V = self.randn_bf16(n, KS)
+            self.torch.cuda.synchronize()
+            ctx.kv_append_device(layer, s, n, K.data_ptr(), V.data_ptr(), zn.data_ptr())
+            ctx.synchronize()
+
+    def token_inputs(self, n=16):
+        """n sets of (q, k, v) for one token, and unit-gain norm weights."""
+        qkv = [(self.randn_bf16(QS), self.randn_bf16(KS), self.randn_bf16(KS)) for _ in range(n)]
+        zn = self.torch.zeros(D, dtype=self.torch.int16, device=self.dev)
+        self.torch.cuda.synchronize()
+        return qkv, zn
+
+    def time_calls(self, stream_ctx, calls, steps, warmup):
+        """Run `calls[i % len]` for warmup + steps; events on the library stream.
+        Returns (region seconds, mean per-launch-group seconds)."""
+        torch = self.torch
+        s = torch.cuda.ExternalStream(stream_ctx.stream())
+        for i in range(warmup):
+            calls[i % len(calls)]()
+        stream_ctx.synchronize()
+        torch.cuda.synchronize()
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            starts[i].record(s)
+            calls[(warmup + i) % len(calls)]()
+            ends[i].record(s)
+        stream_ctx.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        region = starts[0].elapsed_time(ends[-1]) * 1e-3
+        per = [a.elapsed_time(b) * 1e-3 for a, b in zip(starts, ends)]
+        return region, float(np.mean(per)), wall
+
+    # ---------------------------------------------------------------- decode
+    def decode_calls(self, targets, pos, qkv, zn, out):
+        """targets: list of (ctx, layer).  One call per target, inputs rotating."""
+        calls = []
+        for i, (ctx, layer) in enumerate(targets):
+            q, k, v = qkv[i % len(qkv)]
+
+            def f(ctx=ctx, layer=layer, q=q, k=k, v=v):
+                ctx.decode_device(layer, pos, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                  zn.data_ptr(), zn.data_ptr(), out.data_ptr())
+            calls.append(f)
+        return calls
+
+
+def cpu_baseline(L=8192, reps=20):
+    """The reference's attention section on one host core (oracle/_ref)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import g3_oracle as O
+    kind = "reference" if O.have_ref() else "port"
+    pos = L - 1
+    K = O.gen_normal_bf16(L * KS, O.seed_for(2, 2)).reshape(L, KS)
+    V = O.gen_normal_bf16(L * KS, O.seed_for(2, 3)).reshape(L, KS)
+    zn = O.zero_norm()
+    q = O.gen_normal_bf16(QS, O.seed_for(2, 1))
+    k, v = K[pos].copy(), V[pos].copy()
+    cfg = O.Config(max_context=L)
+    if kind == "reference":
+        t = O.rope_table(L, 1e6, use_ref=True)
+        O.norm_rope_batch(K, t, 0, zn)  # rows as the cache holds them
+        zp = zn.ctypes.data_as(C.c_void_p)
+        sec = O.ref().ref_time_decode(q, k, v, zp, zp, K, V, t, HQ, HKV, 5, pos, L, 1024, 3, reps)
+    else:
+        t = O.rope_table(L, 1e6)
+        O.norm_rope_batch(K, t, 0, zn)
+        ts = []
+        for r in range(reps + 3):
+            Kc, Vc = K.copy(), V.copy()
+            a = time.perf_counter()
+            O.layer_decode(cfg, 5, pos, q, k, v, Kc, Vc, t, zn, zn)
+            if r >= 3:
+                ts.append(time.perf_counter() - a)
+        sec = float(np.median(ts))
+    try:
+        cpu_model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
+    except Exception:
+        cpu_model = "unknown"
+    return {
+        "value": round(decode_bytes(L) / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"median of {reps} decode steps (configs[1]: L={L}, pos {pos}) after 3 warm-up, "
+                   f"{sec * 1e6:.0f} us/step, 1 thread ({cpu_model}; nproc {os.cpu_count()}); "
+                   "reference gemma3_kernels.c + gemma3_transformer.c built with "
+                   "-O3 -march=x86-64-v3 -ffast-math, no BLAS (cblas.h absent)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of extra sections to run")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by KV head or by sequence, see DESIGN.md, but no multi-GPU "
+              "figure is produced)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    G = load_binding()
+    B = Bench(G, torch)
+    only = set(filter(None, args.only.split(",")))
+    extra = {}
+
+    # ---------------- headline: configs[1] global decode, L = 8192
+    L = 8192
+    log("[bench] filling 2 x 34-layer contexts, 10 global layers x 8192 positions")
+    ctxs = [B.context(L) for _ in range(2)]
+    targets = []
+    for ctx in ctxs:
+        for layer in (5, 11, 17, 23, 29):
+            B.fill_layer(ctx, layer, L - 1)
+            targets.append((ctx, layer))
+    qkv, zn = B.token_inputs()
+    out = torch.empty(QS, device=B.dev, dtype=torch.float32)
+    calls = B.decode_calls(targets, L - 1, qkv, zn, out)
+    # all calls go to ctx streams; both contexts are timed through ctx 0's
+    # stream only if they share it, so time each context's calls separately
+    log(f"[bench] headline decode L={L}: warmup {args.warmup}, steps {args.steps}")
+    per_ctx = []
+    for ci, ctx in enumerate(ctxs):
+        cl = [c for c, (cx, _) in zip(calls, targets) if cx is ctx]
+        region, per_launch, wall = B.time_calls(ctx, cl, args.steps, args.warmup)
+        per_ctx.append((region, per_launch))
+    region = float(np.mean([r for r, _ in per_ctx]))
+    kernel_s = float(np.mean([p for _, p in per_ctx]))
+    ms_per_step = region / args.steps * 1e3
+    value = decode_bytes(L) / (region / args.steps) / 1e9
+    achieved = decode_bytes(L) / kernel_s / 1e9
+    log(f"[bench] headline: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s; "
+        f"kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
+    for c in ctxs:
+        c.close()
+    del ctxs, targets, calls
+
+    # ---------------- local decode at pos 511 (L = 512)
+    if not only or "local512" in only:
+        ctx = B.context(8192)
+        locs = [l for l in range(34) if not G.is_global_layer(l)]
+        for l in locs:
+            B.fill_layer(ctx, l, 511)
+        cl = B.decode_calls([(ctx, l) for l in locs], 511, qkv, zn, out)
+        region, per, _ = B.time_calls(ctx, cl, 200, 20)
+        extra["decode_local_L512"] = {
+            "config": "configs[0]: local layer, pos 511, L=512, theta 1e4",
+            "us_per_call": round(region / 200 * 1e6, 2),
+            "kernel_us": round(per * 1e6, 2),
+            "GB/s": round(decode_bytes(512) / (region / 200) / 1e9, 1),
+            "bytes_per_call": decode_bytes(512),
+        }
+        log(f"[bench] local512: {extra['decode_local_L512']}")
+        ctx.close()
+
+    # ---------------- 128K: single global layer and the 34-layer stack
+    if not only or "128k" in only or "stack" in only:
+        L = 131072
+        log("[bench] filling a 36-layer context at max_context 131072 (6 global layers)")
+        ctx = B.context(L, num_layers=36)
+        glob = [l for l in range(36) if G.is_global_layer(l)]
+        locs = [l for l in range(36) if not G.is_global_layer(l)]
+        for l in glob:
+            B.fill_layer(ctx, l, L - 1)
+        for l in locs:
+            B.fill_layer(ctx, l, 1024)
+        pos = L - 1
+        cl = B.decode_calls([(ctx, l) for l in glob], pos, qkv, zn, out)
+        region, per, _ = B.time_calls(ctx, cl, 60, 6)
+        extra["decode_global_L131072"] = {
+            "config": "global layer, pos 131071, L=131072, theta 1e6; 6 distinct 1 GiB caches rotated",
+            "us_per_call": round(region / 60 * 1e6, 2),
+            "kernel_us": round(per * 1e6, 2),
+            "GB/s": round(decode_bytes(L) / (region / 60) / 1e9, 1),
+            "kernel_GB/s": round(decode_bytes(L) / per / 1e9, 1),
+            "frac_of_hbm_peak": round(decode_bytes(L) / per / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_call": decode_bytes(L),
+        }
+        log(f"[bench] 128k: {extra['decode_global_L131072']}")
+        # 34-layer stack: one token through every layer's attention
+        for name, layers in (("reference_29local_5global", list(range(34))),
+                             ("literal_28local_6global", glob + locs[:28])):
+            layers = sorted(layers)
+            byts = sum(decode_bytes(L if G.is_global_layer(l) else 1024) for l in layers)
+            cl = B.decode_calls([(ctx, l) for l in layers], pos, qkv, zn, out)
+
+            def step(cl=cl):
+                for f in cl:
+                    f()
+            region, per, _ = B.time_calls(ctx, [step], 20, 3)
+            extra[f"decode_stack34_L131072_{name}"] = {
+                "config": f"configs[4]: 34 layers ({name}), pos 131071",
+                "us_per_token": round(region / 20 * 1e6, 1),
+                "GB/s": round(byts / (region / 20) / 1e9, 1),
+                "frac_of_hbm_peak": round(byts / (region / 20) / 1e9 / HBM_PEAK_GBS, 4),
+                "bytes_per_token": byts,
+            }
+            log(f"[bench] stack {name}: {extra[f'decode_stack34_L131072_{name}']}")
+        ctx.close()
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline (reference code, 1 core)")
+        cpu = cpu_baseline()
+        log(f"[bench] cpu: {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) rounded to bf16, unit-gain QK-norm, RoPE theta 1e6",
+        "config": {
+            "workload": "configs[1]: global-layer decode attention, batch 1, pos 8191, L=8192, "
+                        "8 Q / 4 KV heads, head_dim 256, fp32 KV cache",
+            "us_per_token": round(ms_per_step * 1e3, 3),
+            "bytes_per_step": decode_bytes(8192),
+            "llc": "10 distinct 64 MiB caches rotated (640 MiB > 256 MB Infinity Cache)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_kernel<2,true>",
+            "kernel_us": round(kernel_s * 1e6, 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -16,12 +16,15 @@
 //   one cache row per sub-step, lane c covering dims c*4 + 64*j + e (j, e < 4),
 //   so one load instruction moves 4 rows x 256 contiguous bytes (dwordx4), and
 //   the RoPE partner dim i+128 (j+2) lives in the same lane.
-//   Per step a wave streams 16 consecutive rows (16 KiB of K + 16 KiB of V).
+//   Per step a wave streams 4*R consecutive rows (R rows per lane-group).
 //   Dot products reduce over 16 lanes with four DPP adds; the running max is
 //   kept per query head and wave-uniform (two cross-group shuffles per step).
 //   Softmax runs in the exp2 domain: q is pre-scaled by scale*log2(e).
-//   Waves merge through LDS; workgroups write (m, l, acc) partials and the
-//   last workgroup of each KV head (atomic counter, self-resetting) combines.
+//   Waves merge through LDS; with more than one split each workgroup writes
+//   an (m, l, acc) partial and a second small launch (combine_kernel)
+//   merges them.  A last-arrival combine inside the kernel would need a
+//   device-scope release fence per workgroup, and on gfx950 that writes
+//   back the XCD's whole L2: measured slower than the extra launch.
 #include <hip/hip_runtime.h>
 
 #include "g3k.h"
@@ -34,7 +37,9 @@ using namespace g3k;
 constexpr int D = G3K_HEAD_DIM;
 constexpr int NT = 256;               // threads per workgroup
 constexpr int NW = NT / 64;           // waves per workgroup
-constexpr int ROWS_PER_WAVE_STEP = 16;
+// Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
+// one row so its larger q / acc arrays fit without spills.
+template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 constexpr float NEG_BIG = -1.0e30f;   // "no row seen yet": finite so exp2 never sees inf - inf
 
 // x: this lane's 16 dims of one 256-vector (lane c: dims c*4 + 64j + e).
@@ -85,15 +90,65 @@ __device__ __forceinline__ void store16(float *dst, const float (&x)[4][4], int 
         *reinterpret_cast<float4 *>(dst + c * 4 + 64 * j) = make_float4(x[j][0], x[j][1], x[j][2], x[j][3]);
 }
 
+
+template <int R>
+__device__ __forceinline__ void load_step(float (&kk)[R][4][4], float (&vv)[R][4][4],
+                                          const float *kbase, const float *vbase, long long rs,
+                                          int base, int c1, int skip, int grp, int c) {
+    const int base_row = base + (base >= skip);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int idx = base + grp * R + r;
+        const int row = idx < c1 ? idx + (idx >= skip) : base_row;
+        load16(kk[r], kbase + (size_t)row * rs, c);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int idx = base + grp * R + r;
+        const int row = idx < c1 ? idx + (idx >= skip) : base_row;
+        load16(vv[r], vbase + (size_t)row * rs, c);
+    }
+}
+
+// Write a merged result: normalised output, or an (m, l, acc) partial.
+template <int G>
+__device__ __forceinline__ void emit(const float *s_res, const float *s_resml, float *out,
+                                     float *acc, float *ml) {
+    for (int e = threadIdx.x; e < G * D; e += NT) {
+        const int g = e / D;
+        if (out) {
+            out[e] = s_res[e] / s_resml[g * 2 + 1];
+        } else {
+            acc[e] = s_res[e];
+            if (e % D == 0) {
+                ml[g * 2] = s_resml[g * 2];
+                ml[g * 2 + 1] = s_resml[g * 2 + 1];
+            }
+        }
+    }
+}
+
 template <int G, bool FUSED>
 __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
+    constexpr int R = rows_for<G>();
+    constexpr int ROWS_PER_WAVE_STEP = 4 * R;
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = lane >> 4, c = lane & 15;
 
-    __shared__ float s_acc[NW][G][D];
+    __shared__ float s_acc[NW][G * D];
     __shared__ float s_m[NW][G], s_l[NW][G];
-    __shared__ float s_ml[G3K_MAX_SPLITS * G * 2];
-    __shared__ unsigned s_last;
+    __shared__ float s_res[G * D];
+    __shared__ float s_resml[G * 2];
+
+    const float *kbase = p.kc + (size_t)kvh * p.head_stride;
+    const float *vbase = p.vc + (size_t)kvh * p.head_stride;
+    const int c0 = split * p.rows_per_split;
+    const int c1 = min(c0 + p.rows_per_split, p.n_stream);
+
+    // ---- first step's K/V loads go out before the query prologue ----
+    float kk[R][4][4], vv[R][4][4];
+    int base = c0 + wave * ROWS_PER_WAVE_STEP;
+    if (base < c1) load_step(kk, vv, kbase, vbase, p.row_stride, base, c1, p.skip, grp, c);
 
     // ---- query: this lane's 16 dims of each of the G query heads ----
     float qv[G][4][4];
@@ -128,9 +183,6 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
             for (int e = 0; e < 4; e++) acc[g][j][e] = 0.f;
     }
 
-    float *kbase = p.kc + (size_t)kvh * p.head_stride;
-    float *vbase = p.vc + (size_t)kvh * p.head_stride;
-
     // ---- the new token (fused decode): split 0, wave 0 seeds its state with it ----
     if (FUSED && split == 0 && wave == 0) {
         float kn[4][4], vn[4][4];
@@ -138,8 +190,8 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         load16(vn, p.v_new + (size_t)kvh * D, c);
         norm_rope16(kn, p.q_norm ? p.k_norm : nullptr, p.eps, cs, sn, c);
         if (grp == 0) {
-            store16(kbase + (size_t)p.new_slot * p.row_stride, kn, c);
-            store16(vbase + (size_t)p.new_slot * p.row_stride, vn, c);
+            store16(p.kc + (size_t)kvh * p.head_stride + (size_t)p.new_slot * p.row_stride, kn, c);
+            store16(p.vc + (size_t)kvh * p.head_stride + (size_t)p.new_slot * p.row_stride, vn, c);
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -159,31 +211,20 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         }
     }
 
-    // ---- stream this split's rows ----
-    const int c0 = split * p.rows_per_split;
-    const int c1 = min(c0 + p.rows_per_split, p.n_stream);
-    for (int base = c0 + wave * ROWS_PER_WAVE_STEP; base < c1; base += NW * ROWS_PER_WAVE_STEP) {
-        const int base_row = base + (base >= p.skip);
-        float kk[4][4][4], vv[4][4][4];
-        bool valid[4];
-        int idx[4];
+    // ---- stream this split's rows: compute the loaded step, then load the next ----
+    while (base < c1) {
+        bool valid[R];
+        int idx[R];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            idx[r] = base + grp * 4 + r;
+        for (int r = 0; r < R; r++) {
+            idx[r] = base + grp * R + r;
             valid[r] = idx[r] < c1;
-            const int row = valid[r] ? idx[r] + (idx[r] >= p.skip) : base_row;
-            load16(kk[r], kbase + (size_t)row * p.row_stride, c);
         }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = valid[r] ? idx[r] + (idx[r] >= p.skip) : base_row;
-            load16(vv[r], vbase + (size_t)row * p.row_stride, c);
-        }
-        float s[G][4];
+        float s[G][R];
 #pragma unroll
         for (int g = 0; g < G; g++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
+            for (int r = 0; r < R; r++) {
                 float d = 0.f;
 #pragma unroll
                 for (int j = 0; j < 4; j++)
@@ -192,7 +233,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
                 s[g][r] = row16_sum(d);
             }
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
+        for (int r = 0; r < R; r++) {
             float add = 0.f;
             if (!FUSED && p.mask && valid[r]) add = p.mask[idx[r]] * 1.4426950408889634f;
 #pragma unroll
@@ -200,26 +241,33 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         }
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            float mx = fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3]));
+            float mx = s[g][0];
+#pragma unroll
+            for (int r = 1; r < R; r++) mx = fmaxf(mx, s[g][r]);
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float mn = fmaxf(m[g], mx);
             const float alpha = fast_exp2(m[g] - mn);
             m[g] = mn;
-            float pr[4];
+            float pr[R], psum = 0.f;
 #pragma unroll
-            for (int r = 0; r < 4; r++) pr[r] = fast_exp2(s[g][r] - mn);
-            l[g] = l[g] * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+            for (int r = 0; r < R; r++) {
+                pr[r] = fast_exp2(s[g][r] - mn);
+                psum += pr[r];
+            }
+            l[g] = l[g] * alpha + psum;
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float a = acc[g][j][e] * alpha;
 #pragma unroll
-                    for (int r = 0; r < 4; r++) a += pr[r] * vv[r][j][e];
+                    for (int r = 0; r < R; r++) a += pr[r] * vv[r][j][e];
                     acc[g][j][e] = a;
                 }
         }
+        base += NW * ROWS_PER_WAVE_STEP;
+        if (base < c1) load_step(kk, vv, kbase, vbase, p.row_stride, base, c1, p.skip, grp, c);
     }
 
     // ---- merge the four lane-groups of each wave (they share m) ----
@@ -239,7 +287,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     }
     if (grp == 0) {
 #pragma unroll
-        for (int g = 0; g < G; g++) store16(&s_acc[wave][g][0], acc[g], c);
+        for (int g = 0; g < G; g++) store16(&s_acc[wave][g * D], acc[g], c);
     }
     if (lane == 0) {
 #pragma unroll
@@ -251,9 +299,8 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     __syncthreads();
 
     // ---- merge the waves: this workgroup's (m, l, acc) per query head ----
-    const bool single = p.n_splits == 1;
     for (int e = tid; e < G * D; e += NT) {
-        const int g = e / D, d = e % D;
+        const int g = e / D;
         float M = s_m[0][g];
 #pragma unroll
         for (int w = 1; w < NW; w++) M = fmaxf(M, s_m[w][g]);
@@ -262,65 +309,108 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         for (int w = 0; w < NW; w++) {
             const float f = fast_exp2(s_m[w][g] - M);
             L += s_l[w][g] * f;
-            A += s_acc[w][g][d] * f;
+            A += s_acc[w][e] * f;
         }
-        if (single) {
-            p.out[(size_t)(kvh * G + g) * D + d] = A / L;
-        } else {
-            const size_t slot = ((size_t)kvh * p.n_splits + split) * G + g;
-            p.ws_acc[slot * D + d] = A;
-            if (d == 0) {
-                p.ws_ml[slot * 2] = M;
-                p.ws_ml[slot * 2 + 1] = L;
-            }
+        s_res[e] = A;
+        if (e % D == 0) {
+            s_resml[g * 2] = M;
+            s_resml[g * 2 + 1] = L;
         }
     }
-    if (single) return;
+    __syncthreads();
+    float *out = p.out + (size_t)kvh * G * D;
+    if (p.n_splits == 1) {
+        emit<G>(s_res, s_resml, out, nullptr, nullptr);
+        return;
+    }
+    // ---- this split's partial; combine_kernel merges the splits ----
+    const size_t slot = (size_t)kvh * G3K_MAX_SPLITS + split;
+    emit<G>(s_res, s_resml, nullptr, p.ws_acc + slot * G * D, p.ws_ml + slot * G * 2);
+}
 
-    // ---- last workgroup of this KV head combines all splits ----
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&p.counters[kvh], 1u) == (unsigned)(p.n_splits - 1);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+// Cross-split combine, one launch after decode_kernel (kernel order makes
+// the partials visible; no fences or atomics).  grid (D / 64, group, H_kv),
+// 256 threads: wave w takes splits w, w+4, ...; lane l owns dim 64*x + l.
+template <int G>
+__global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
+    const int x = blockIdx.x, g = blockIdx.y, kvh = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int d = 64 * x + lane;
+    __shared__ float s_a[NW][64], s_m[NW], s_l[NW];
     const int S = p.n_splits;
-    const float *ml = p.ws_ml + (size_t)kvh * S * G * 2;
-    for (int i = tid; i < S * G * 2; i += NT) s_ml[i] = __builtin_nontemporal_load(ml + i);
-    __syncthreads();
-    for (int e = tid; e < G * D; e += NT) {
-        const int g = e / D, d = e % D;
-        float M = NEG_BIG;
-        for (int s = 0; s < S; s++) M = fmaxf(M, s_ml[(s * G + g) * 2]);
-        float L = 0.f, A = 0.f;
-        const float *src = p.ws_acc + ((size_t)kvh * S * G + g) * D + d;
+    const size_t slot0 = (size_t)kvh * G3K_MAX_SPLITS;
+    float M = NEG_BIG, L = 0.f, A = 0.f;
 #pragma unroll 8
-        for (int s = 0; s < S; s++) {
-            const float f = fast_exp2(s_ml[(s * G + g) * 2] - M);
-            L += s_ml[(s * G + g) * 2 + 1] * f;
-            A += __builtin_nontemporal_load(src + (size_t)s * G * D) * f;
-        }
-        p.out[(size_t)(kvh * G + g) * D + d] = A / L;
+    for (int q = wave; q < S; q += NW) {
+        const size_t sl = (slot0 + q) * G + g;
+        const float m = p.ws_ml[sl * 2], lw = p.ws_ml[sl * 2 + 1];
+        const float v = p.ws_acc[sl * D + d];
+        const float mn = fmaxf(M, m);
+        const float a = fast_exp2(M - mn), b = fast_exp2(m - mn);
+        L = L * a + lw * b;
+        A = A * a + v * b;
+        M = mn;
     }
-    if (tid == 0) atomicExch(&p.counters[kvh], 0u);
+    s_a[wave][lane] = A;
+    if (lane == 0) {
+        s_m[wave] = M;
+        s_l[wave] = L;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float Mx = s_m[0];
+#pragma unroll
+        for (int w = 1; w < NW; w++) Mx = fmaxf(Mx, s_m[w]);
+        float Lx = 0.f, Ax = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = fast_exp2(s_m[w] - Mx);
+            Lx += s_l[w] * f;
+            Ax += s_a[w][lane] * f;
+        }
+        p.out[((size_t)kvh * G + g) * D + d] = Ax / Lx;
+    }
 }
 
 template <int G, bool FUSED>
 hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
     dim3 grid(a->n_splits, a->n_kv_heads);
     hipLaunchKernelGGL((decode_kernel<G, FUSED>), grid, dim3(NT), 0, st, *a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a->n_splits == 1) return e;
+    hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 64, G, a->n_kv_heads), dim3(NT), 0, st, *a);
     return hipGetLastError();
+}
+
+template <int G, bool FUSED>
+int capacity() {
+    int per_cu = 0, cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<G, FUSED>, NT, 0) != hipSuccess)
+        return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return per_cu * cus;
 }
 
 }  // namespace
 
 extern "C" int g3k_decode(const g3k_decode_args *a, int fused, void *stream) {
     hipStream_t st = (hipStream_t)stream;
-    if (a->n_splits < 1 || a->n_splits > G3K_MAX_SPLITS || a->rows_per_split % 64) return (int)hipErrorInvalidValue;
+    if (a->n_splits < 1 || a->n_splits > G3K_MAX_SPLITS || a->rows_per_split % 64)
+        return (int)hipErrorInvalidValue;
     switch (a->group) {
         case 1: return (int)(fused ? launch<1, true>(a, st) : launch<1, false>(a, st));
         case 2: return (int)(fused ? launch<2, true>(a, st) : launch<2, false>(a, st));
         case 4: return (int)(fused ? launch<4, true>(a, st) : launch<4, false>(a, st));
         default: return (int)hipErrorInvalidValue;
+    }
+}
+
+extern "C" int g3k_decode_capacity(int group, int fused) {
+    switch (group) {
+        case 1: return fused ? capacity<1, true>() : capacity<1, false>();
+        case 2: return fused ? capacity<2, true>() : capacity<2, false>();
+        case 4: return fused ? capacity<4, true>() : capacity<4, false>();
+        default: return 0;
     }
 }

@@ -46,14 +46,18 @@ typedef struct {
     int group;             /* query heads per kv head: 1, 2 or 4 */
     /* outputs */
     float *out;            /* [H_q][D] */
-    float *ws_acc;         /* [H_kv][n_splits][group][D] */
-    float *ws_ml;          /* [H_kv][n_splits][group][2] */
-    unsigned *counters;    /* [H_kv], zero between launches */
+    float *ws_acc;         /* [H_kv][G3K_MAX_SPLITS][group][D] split partials */
+    float *ws_ml;          /* [H_kv][G3K_MAX_SPLITS][group][2] (max, sum) */
 } g3k_decode_args;
 
-/* One launch: QK-norm + RoPE of q (and of the new k), cache write of the new
- * k/v, split-K attention over the cache and the cross-split combine. */
+/* QK-norm + RoPE of q (and of the new k), cache write of the new k/v and
+ * split-K attention over the cache; with n_splits > 1 a second launch
+ * combines the split partials. */
 int g3k_decode(const g3k_decode_args *a, int fused, void *stream);
+
+/* Workgroups of the decode kernel that can be resident at once on the
+ * current device (occupancy x compute units); 0 if unknown. */
+int g3k_decode_capacity(int group, int fused);
 
 /* Batched QK-norm + RoPE + cache write for n tokens (positions start_pos..).
  *   Q [n][H_q][D] (may be NULL) -> q_out head-major [H_q][n][D];

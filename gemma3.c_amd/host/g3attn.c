@@ -97,7 +97,6 @@ struct g3attn_ctx {
     float **kc, **vc;
     int *rows;
     float *ws_acc, *ws_ml;
-    unsigned *counters;
     /* staging of the host-pointer decode: q | k | v | q_norm | k_norm, and out */
     unsigned char *h_in, *d_in;
     float *h_out, *d_out;
@@ -106,6 +105,7 @@ struct g3attn_ctx {
     void *d_big;
     size_t d_big_cap;
     int split_rows; /* 0 = heuristic */
+    int target_wgs; /* decode workgroups per call (all KV heads) */
 };
 
 static void ctx_free(g3attn_ctx *c) {
@@ -121,7 +121,6 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->rope_global);
     hipFree(c->ws_acc);
     hipFree(c->ws_ml);
-    hipFree(c->counters);
     hipFree(c->d_in);
     hipFree(c->d_out);
     hipFree(c->d_big);
@@ -141,9 +140,9 @@ static int alloc_dev(void **p, size_t bytes, const char *what) {
     return 1;
 }
 
-static size_t ws_floats(const g3attn_ctx *c) {
-    return (size_t)c->cfg.num_kv_heads * G3K_MAX_SPLITS * c->group * D;
-}
+/* Decode combine workspace: split slots [H_kv][G3K_MAX_SPLITS], each
+ * group * head_dim floats (+ group * 2 for max and sum). */
+static size_t ws_slots(int n_kv) { return (size_t)n_kv * G3K_MAX_SPLITS; }
 
 g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
                           const float *rope_local, const float *rope_global) {
@@ -201,10 +200,15 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         if (hipMemset(c->kc[l], 0, bytes) != hipSuccess || hipMemset(c->vc[l], 0, bytes) != hipSuccess)
             goto fail_rt;
     }
-    if (!alloc_dev((void **)&c->ws_acc, ws_floats(c) * sizeof(float), "decode workspace")) goto fail;
-    if (!alloc_dev((void **)&c->ws_ml, ws_floats(c) / D * 2 * sizeof(float), "decode workspace")) goto fail;
-    if (!alloc_dev((void **)&c->counters, (size_t)cfg->num_kv_heads * sizeof(unsigned), "counters")) goto fail;
-    if (hipMemset(c->counters, 0, (size_t)cfg->num_kv_heads * sizeof(unsigned)) != hipSuccess) goto fail_rt;
+    const size_t slots = ws_slots(cfg->num_kv_heads) * c->group;
+    if (!alloc_dev((void **)&c->ws_acc, slots * D * sizeof(float), "decode workspace")) goto fail;
+    if (!alloc_dev((void **)&c->ws_ml, slots * 2 * sizeof(float), "decode workspace")) goto fail;
+    {
+        const char *w = getenv("G3ATTN_DECODE_WGS");
+        int cus = 0;
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device);
+        c->target_wgs = w ? atoi(w) : (cus > 0 ? cus : 256);
+    }
 
     const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D;
     c->in_bytes = (qs + 2 * ks) * sizeof(float) + 2 * D * sizeof(uint16_t);
@@ -260,21 +264,20 @@ static int grow_big(g3attn_ctx *c, size_t bytes) {
 
 /* ------------------------------------------------------------------ decode */
 
-/* Split-K shape: about 1024 workgroups over all KV heads, at least 128 rows
- * per workgroup (two 16-row steps per wave), at most G3K_MAX_SPLITS splits. */
-static void choose_splits(int n_stream, int n_kv, int override_rows, int *rps, int *ns) {
+/* Split-K shape: about one resident wave of workgroups (capacity =
+ * occupancy x CUs, G3ATTN_DECODE_WGS overrides) spread over the KV heads, at
+ * least 256 rows per workgroup, at most G3K_MAX_SPLITS splits per head. */
+static void choose_splits(int n_stream, int n_kv, int target_wgs, int override_rows,
+                          g3k_decode_args *a) {
     if (n_stream <= 0) {
-        *rps = 64;
-        *ns = 1;
+        a->rows_per_split = 64;
+        a->n_splits = 1;
         return;
     }
-    long r;
-    if (override_rows > 0) {
-        r = override_rows;
-    } else {
-        r = ((long)n_stream * n_kv + 1023) / 1024;
-        if (r < 128) r = 128;
-    }
+    long per_head = (target_wgs > 0 ? target_wgs : 256) / n_kv;
+    if (per_head < 1) per_head = 1;
+    long r = override_rows > 0 ? override_rows : (n_stream + per_head - 1) / per_head;
+    if (override_rows <= 0 && r < 256) r = 256;
     r = (r + 63) / 64 * 64;
     long s = (n_stream + r - 1) / r;
     if (s > G3K_MAX_SPLITS) {
@@ -282,8 +285,8 @@ static void choose_splits(int n_stream, int n_kv, int override_rows, int *rps, i
         r = (r + 63) / 64 * 64;
         s = (n_stream + r - 1) / r;
     }
-    *rps = (int)r;
-    *ns = (int)s;
+    a->rows_per_split = (int)r;
+    a->n_splits = (int)s;
 }
 
 static int check_layer(const g3attn_ctx *c, int layer, const char *fn) {
@@ -334,13 +337,12 @@ int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, cons
     a.new_slot = slot;
     a.mask = NULL;
     a.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
-    choose_splits(a.n_stream, c->cfg.num_kv_heads, c->split_rows, &a.rows_per_split, &a.n_splits);
+    choose_splits(a.n_stream, c->cfg.num_kv_heads, c->target_wgs, c->split_rows, &a);
     a.n_kv_heads = c->cfg.num_kv_heads;
     a.group = c->group;
     a.out = attn_out;
     a.ws_acc = c->ws_acc;
     a.ws_ml = c->ws_ml;
-    a.counters = c->counters;
     hipSetDevice(c->device);
     const int rc = g3k_decode(&a, 1, c->stream);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_decode launch");
@@ -518,8 +520,7 @@ static struct {
     void *buf;
     size_t cap;
     float *ws_acc, *ws_ml;
-    unsigned *counters;
-} g_gqa = {PTHREAD_MUTEX_INITIALIZER, 0, 0, NULL, NULL, 0, NULL, NULL, NULL};
+} g_gqa = {PTHREAD_MUTEX_INITIALIZER, 0, 0, NULL, NULL, 0, NULL, NULL};
 
 #define GQA_MAX_KV 64
 
@@ -527,12 +528,10 @@ static int gqa_init(void) {
     if (g_gqa.ready) return G3_OK;
     HIP_TRY(hipGetDevice(&g_gqa.device), "g3attn_gqa init");
     HIP_TRY(hipStreamCreateWithFlags(&g_gqa.stream, hipStreamNonBlocking), "g3attn_gqa init");
-    const size_t wsf = (size_t)GQA_MAX_KV * G3K_MAX_SPLITS * 4 * D;
-    if (!alloc_dev((void **)&g_gqa.ws_acc, wsf * sizeof(float), "gqa workspace") ||
-        !alloc_dev((void **)&g_gqa.ws_ml, wsf / D * 2 * sizeof(float), "gqa workspace") ||
-        !alloc_dev((void **)&g_gqa.counters, GQA_MAX_KV * sizeof(unsigned), "gqa counters"))
+    const size_t slots = ws_slots(GQA_MAX_KV) * 4; /* group <= 4 */
+    if (!alloc_dev((void **)&g_gqa.ws_acc, slots * D * sizeof(float), "gqa workspace") ||
+        !alloc_dev((void **)&g_gqa.ws_ml, slots * 2 * sizeof(float), "gqa workspace"))
         return G3_ERR_OUT_OF_MEMORY;
-    HIP_TRY(hipMemset(g_gqa.counters, 0, GQA_MAX_KV * sizeof(unsigned)), "g3attn_gqa init");
     g_gqa.ready = 1;
     return G3_OK;
 }
@@ -581,13 +580,12 @@ static int gqa_run(float *output, const float *q, const float *k_cache, const fl
     a.new_slot = -1;
     a.mask = dm;
     a.qscale = scale * LOG2E;
-    choose_splits(seq_len, n_kv, 0, &a.rows_per_split, &a.n_splits);
+    choose_splits(seq_len, n_kv, 256, 0, &a);
     a.n_kv_heads = n_kv;
     a.group = n_heads / n_kv;
     a.out = dout;
     a.ws_acc = g_gqa.ws_acc;
     a.ws_ml = g_gqa.ws_ml;
-    a.counters = g_gqa.counters;
     rc = g3k_decode(&a, 0, s);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa launch");
     HIP_TRY(hipMemcpyAsync(output, dout, qs * 4, hipMemcpyDeviceToHost, s), "g3attn_gqa download");

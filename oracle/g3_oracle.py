@@ -142,6 +142,10 @@ def ref():
                                        _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int]
         R.ref_prefill_loop.restype = C.c_int
+        R.ref_time_decode.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _f32p, _f32p,
+                                      _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, C.c_int]
+        R.ref_time_decode.restype = C.c_double
         _ref = R
     return _ref
 

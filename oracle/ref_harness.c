@@ -18,9 +18,11 @@
  * ref_prefill_loop restates only its loop skeleton and calls the
  * reference's own rmsnorm / rope / cache_kv / causal_mask / gqa.
  */
+#define _POSIX_C_SOURCE 199309L /* clock_gettime under -std=c11 */
 #include "gemma3_transformer.c"
 
 #include <stdint.h>
+#include <time.h>
 
 #define RH_D 256
 
@@ -156,4 +158,37 @@ int ref_prefill_loop(float *attn_out, float *Q, float *K, const float *V,
     free(mask);
     free(scores);
     return 0;
+}
+
+/* Time `reps` decode steps of the reference attention section (the n = 1 case
+ * of ref_prefill_loop: norm, RoPE, cache_kv, mask, gemma3_gqa) at position pos
+ * against caller-filled caches; returns the median seconds per step.  q, k are
+ * restored from the inputs before every step. */
+static int cmp_double(const void *a, const void *b) {
+    double x = *(const double *)a, y = *(const double *)b;
+    return (x > y) - (x < y);
+}
+double ref_time_decode(const float *q, const float *k, const float *v, const uint16_t *q_norm,
+                       const uint16_t *k_norm, float *k_cache, float *v_cache, const float *rope,
+                       int hq, int hkv, int layer, int pos, int max_context, int window,
+                       int warmup, int reps) {
+    const int qs = hq * RH_D, ks = hkv * RH_D;
+    float *qb = (float *)malloc((size_t)qs * 4), *kb = (float *)malloc((size_t)ks * 4);
+    float *out = (float *)malloc((size_t)qs * 4);
+    double *t = (double *)malloc((size_t)(reps > 0 ? reps : 1) * sizeof(double));
+    if (!qb || !kb || !out || !t) return -1.0;
+    for (int r = -warmup; r < reps; r++) {
+        memcpy(qb, q, (size_t)qs * 4);
+        memcpy(kb, k, (size_t)ks * 4);
+        struct timespec a, b;
+        clock_gettime(CLOCK_MONOTONIC, &a);
+        ref_prefill_loop(out, qb, kb, v, q_norm, k_norm, k_cache, v_cache, rope, hq, hkv, layer,
+                         pos, 1, max_context, window);
+        clock_gettime(CLOCK_MONOTONIC, &b);
+        if (r >= 0) t[r] = (b.tv_sec - a.tv_sec) + 1e-9 * (b.tv_nsec - a.tv_nsec);
+    }
+    qsort(t, (size_t)reps, sizeof(double), cmp_double);
+    const double med = reps > 0 ? t[reps / 2] : 0.0;
+    free(qb); free(kb); free(out); free(t);
+    return med;
 }

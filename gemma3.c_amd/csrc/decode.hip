@@ -40,7 +40,11 @@ constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
 // one row so its larger q / acc arrays fit without spills.
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
-constexpr float NEG_BIG = -1.0e30f;   // "no row seen yet": finite so exp2 never sees inf - inf
+constexpr float NEG_BIG = -1.0e30f;
+// Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
+// in flight per wave, one contiguous row range per split.  Double-buffered
+// steps, three workgroups per CU and block-cyclic row assignment were each
+// slower or no faster at both 8K and 128K.   // "no row seen yet": finite so exp2 never sees inf - inf
 
 // x: this lane's 16 dims of one 256-vector (lane c: dims c*4 + 64j + e).
 // RMSNorm with (1 + w) gain (gemma3_kernels.c:289-304), then the NeoX
@@ -128,6 +132,69 @@ __device__ __forceinline__ void emit(const float *s_res, const float *s_resml, f
     }
 }
 
+// One step: scores of this lane-group's R rows for the G query heads (16-lane
+// DPP reduction), online-softmax update with a wave-uniform running max, and
+// the P.V accumulation.
+template <int G, int R, bool FUSED>
+__device__ __forceinline__ void step_compute(const float (&kk)[R][4][4], const float (&vv)[R][4][4],
+                                             const float (&qv)[G][4][4], float (&m)[G], float (&l)[G],
+                                             float (&acc)[G][4][4], int base, int c1, int grp,
+                                             const float *mask) {
+    bool valid[R];
+    int idx[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        idx[r] = base + grp * R + r;
+        valid[r] = idx[r] < c1;
+    }
+    float s[G][R];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) d += qv[g][j][e] * kk[r][j][e];
+            s[g][r] = row16_sum(d);
+        }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float add = 0.f;
+        if (!FUSED && mask && valid[r]) add = mask[idx[r]] * 1.4426950408889634f;
+#pragma unroll
+        for (int g = 0; g < G; g++) s[g][r] = valid[r] ? s[g][r] + add : -INFINITY;
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float mx = s[g][0];
+#pragma unroll
+        for (int r = 1; r < R; r++) mx = fmaxf(mx, s[g][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m[g], mx);
+        const float alpha = fast_exp2(m[g] - mn);
+        m[g] = mn;
+        float pr[R], psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            pr[r] = fast_exp2(s[g][r] - mn);
+            psum += pr[r];
+        }
+        l[g] = l[g] * alpha + psum;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float a = acc[g][j][e] * alpha;
+#pragma unroll
+                for (int r = 0; r < R; r++) a += pr[r] * vv[r][j][e];
+                acc[g][j][e] = a;
+            }
+    }
+}
+
 template <int G, bool FUSED>
 __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     constexpr int R = rows_for<G>();
@@ -144,6 +211,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     const float *vbase = p.vc + (size_t)kvh * p.head_stride;
     const int c0 = split * p.rows_per_split;
     const int c1 = min(c0 + p.rows_per_split, p.n_stream);
+    const int stride = NW * ROWS_PER_WAVE_STEP;
 
     // ---- first step's K/V loads go out before the query prologue ----
     float kk[R][4][4], vv[R][4][4];
@@ -211,62 +279,10 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         }
     }
 
-    // ---- stream this split's rows: compute the loaded step, then load the next ----
+    // ---- stream this split's rows: reduce the loaded step, then load the next ----
     while (base < c1) {
-        bool valid[R];
-        int idx[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            idx[r] = base + grp * R + r;
-            valid[r] = idx[r] < c1;
-        }
-        float s[G][R];
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float d = 0.f;
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) d += qv[g][j][e] * kk[r][j][e];
-                s[g][r] = row16_sum(d);
-            }
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            float add = 0.f;
-            if (!FUSED && p.mask && valid[r]) add = p.mask[idx[r]] * 1.4426950408889634f;
-#pragma unroll
-            for (int g = 0; g < G; g++) s[g][r] = valid[r] ? s[g][r] + add : -INFINITY;
-        }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float mx = s[g][0];
-#pragma unroll
-            for (int r = 1; r < R; r++) mx = fmaxf(mx, s[g][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m[g], mx);
-            const float alpha = fast_exp2(m[g] - mn);
-            m[g] = mn;
-            float pr[R], psum = 0.f;
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                pr[r] = fast_exp2(s[g][r] - mn);
-                psum += pr[r];
-            }
-            l[g] = l[g] * alpha + psum;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float a = acc[g][j][e] * alpha;
-#pragma unroll
-                    for (int r = 0; r < R; r++) a += pr[r] * vv[r][j][e];
-                    acc[g][j][e] = a;
-                }
-        }
-        base += NW * ROWS_PER_WAVE_STEP;
+        step_compute<G, R, FUSED>(kk, vv, qv, m, l, acc, base, c1, grp, p.mask);
+        base += stride;
         if (base < c1) load_step(kk, vv, kbase, vbase, p.row_stride, base, c1, p.skip, grp, c);
     }
 
@@ -339,17 +355,17 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
     __shared__ float s_a[NW][64], s_m[NW], s_l[NW];
     const int S = p.n_splits;
     const size_t slot0 = (size_t)kvh * G3K_MAX_SPLITS;
-    float M = NEG_BIG, L = 0.f, A = 0.f;
+    // pass 1: this wave's max over its splits (small loads, all independent)
+    float M = NEG_BIG;
+    for (int q = wave; q < S; q += NW) M = fmaxf(M, p.ws_ml[((slot0 + q) * G + g) * 2]);
+    // pass 2: weights against that max; loads carry no dependency on the math
+    float L = 0.f, A = 0.f;
 #pragma unroll 8
     for (int q = wave; q < S; q += NW) {
         const size_t sl = (slot0 + q) * G + g;
-        const float m = p.ws_ml[sl * 2], lw = p.ws_ml[sl * 2 + 1];
-        const float v = p.ws_acc[sl * D + d];
-        const float mn = fmaxf(M, m);
-        const float a = fast_exp2(M - mn), b = fast_exp2(m - mn);
-        L = L * a + lw * b;
-        A = A * a + v * b;
-        M = mn;
+        const float b = fast_exp2(p.ws_ml[sl * 2] - M);
+        L += p.ws_ml[sl * 2 + 1] * b;
+        A += p.ws_acc[sl * D + d] * b;
     }
     s_a[wave][lane] = A;
     if (lane == 0) {

@@ -18,7 +18,7 @@ import re
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libg3attn.so")
+LIB_PATH = os.environ.get("G3ATTN_LIB") or os.path.join(HERE, "lib", "libg3attn.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "g3attn.h")
 
 # gemma3_error (gemma3.h:57-67) codes returned by the entry points

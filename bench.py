@@ -15,12 +15,17 @@ position, 4 KV heads x 256 x 4 B x 2) + q in + out = 8192*L + 16384.
 
 `roofline` is for the decode kernel at the headline config: achieved =
 algorithmic bytes / average kernel duration, the duration from paired HIP
-events around every launch on the library's own stream.
+events that the library records around every decode_kernel launch on its own
+stream (g3attn_profile_*; the small split-combine launch is excluded and
+reported separately as part of the per-call time).
 
 Further configs (reported under "extra", not the headline): configs[0] local
 decode L=512, 128K global-layer decode, the 34-layer decode stack at
 pos 131071 (reference 29 local / 5 global pattern and the config's literal
-28 / 6), and prefill when the library has it.
+28 / 6), configs[2] local prefill (N=2048, window 1024) and configs[3]
+global prefill (N=8192).  Prefill FLOPs are algorithmic: 4 * H_q * d * P for
+P attended (query, key) pairs; the MFMA kernel issues 2.5x that (three fp16
+passes for QK^T, two bf16 passes for PV), reported as "issued".
 
 `cpu_baseline`: the reference's own attention code (oracle/_ref, compiled
 from the reference sources with its fast-mode flags, no BLAS) timed on one
@@ -48,6 +53,15 @@ QS, KS = HQ * D, HKV * D
 
 def decode_bytes(L: int) -> int:
     return 8192 * L + 16384
+
+
+def prefill_pairs(n: int, window: int) -> int:
+    """Attended (query, key) pairs of a causal prefill from position 0."""
+    return sum(min(i + 1, window) for i in range(n))
+
+
+def prefill_flops(n: int, window: int) -> float:
+    return 4.0 * HQ * D * prefill_pairs(n, window)
 
 
 def load_binding():
@@ -186,7 +200,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extra sections to run")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run 5 plain device-to-device copies of this many MiB (the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_probe_mib > 0:
+        import torch
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, device="cuda", dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_mib": args.copy_probe_mib, "launches": 5,
+                          "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the path shards by KV head or by sequence, see DESIGN.md, but no multi-GPU "
@@ -221,15 +249,21 @@ def main():
     per_ctx = []
     for ci, ctx in enumerate(ctxs):
         cl = [c for c, (cx, _) in zip(calls, targets) if cx is ctx]
-        region, per_launch, wall = B.time_calls(ctx, cl, args.steps, args.warmup)
-        per_ctx.append((region, per_launch))
-    region = float(np.mean([r for r, _ in per_ctx]))
-    kernel_s = float(np.mean([p for _, p in per_ctx]))
+        for i in range(args.warmup):
+            cl[i % len(cl)]()
+        ctx.profile(True)
+        region, per_call, wall = B.time_calls(ctx, cl, args.steps, 0)
+        kms, kn = ctx.profile_read(0)
+        ctx.profile(False)
+        per_ctx.append((region, per_call, kms * 1e-3 / max(kn, 1)))
+    region = float(np.mean([r for r, _, _ in per_ctx]))
+    call_s = float(np.mean([c for _, c, _ in per_ctx]))
+    kernel_s = float(np.mean([k for _, _, k in per_ctx]))
     ms_per_step = region / args.steps * 1e3
     value = decode_bytes(L) / (region / args.steps) / 1e9
     achieved = decode_bytes(L) / kernel_s / 1e9
-    log(f"[bench] headline: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s; "
-        f"kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
+    log(f"[bench] headline: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s; call {call_s * 1e6:.2f} us; "
+        f"decode_kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
     for c in ctxs:
         c.close()
     del ctxs, targets, calls
@@ -297,6 +331,45 @@ def main():
             log(f"[bench] stack {name}: {extra[f'decode_stack34_L131072_{name}']}")
         ctx.close()
 
+    # ---------------- prefill
+    for name, layer, n, window, steps in (("prefill_local_N2048_w1024", 0, 2048, 1024, 30),
+                                          ("prefill_global_N8192", 5, 8192, 1 << 30, 8)):
+        if only and "prefill" not in only and name not in only:
+            continue
+        ctx = B.context(8192)
+        Q, K, V = B.randn_bf16(n, QS), B.randn_bf16(n, KS), B.randn_bf16(n, KS)
+        zn16 = torch.zeros(D, dtype=torch.int16, device=B.dev)
+        pout = torch.empty(n, QS, device=B.dev, dtype=torch.float32)
+        torch.cuda.synchronize()
+
+        def pf(ctx=ctx, layer=layer, n=n, Q=Q, K=K, V=V, zn16=zn16, pout=pout):
+            ctx.prefill_device(layer, 0, n, Q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                               zn16.data_ptr(), zn16.data_ptr(), pout.data_ptr())
+        for _ in range(3):
+            pf()
+        ctx.profile(True)
+        region, per_call, _ = B.time_calls(ctx, [pf], steps, 0)
+        kms, kn = ctx.profile_read(1)
+        ctx.profile(False)
+        flops = prefill_flops(n, window)
+        k_s = kms * 1e-3 / max(kn, 1)
+        extra[name] = {
+            "config": (f"configs[{2 if layer == 0 else 3}]: {'local' if layer == 0 else 'global'} "
+                       f"prefill, N={n}, start 0" + (f", window {window}" if window < n else "")),
+            "us_per_call": round(region / steps * 1e6, 1),
+            "kernel_us": round(k_s * 1e6, 1),
+            "pairs": prefill_pairs(n, window),
+            "algorithmic_GFLOP": round(flops / 1e9, 3),
+            "algorithmic_TFLOP/s_call": round(flops / (region / steps) / 1e12, 1),
+            "algorithmic_TFLOP/s_kernel": round(flops / k_s / 1e12, 1),
+            "issued_MFMA_TFLOP/s_kernel": round(2.5 * flops / k_s / 1e12, 1),
+            "frac_of_bf16_peak_algorithmic": round(flops / k_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "frac_of_bf16_peak_issued": round(2.5 * flops / k_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        }
+        log(f"[bench] {name}: {extra[name]}")
+        ctx.close()
+        del Q, K, V, pout
+
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (reference code, 1 core)")
@@ -332,6 +405,7 @@ def main():
             "traffic": None,
             "kernel": "decode_kernel<2,true>",
             "kernel_us": round(kernel_s * 1e6, 3),
+            "call_us": round(call_s * 1e6, 3),
         },
         "cpu_baseline": cpu,
         "extra": extra,

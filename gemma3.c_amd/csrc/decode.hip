@@ -355,17 +355,33 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
     __shared__ float s_a[NW][64], s_m[NW], s_l[NW];
     const int S = p.n_splits;
     const size_t slot0 = (size_t)kvh * G3K_MAX_SPLITS;
-    // pass 1: this wave's max over its splits (small loads, all independent)
-    float M = NEG_BIG;
-    for (int q = wave; q < S; q += NW) M = fmaxf(M, p.ws_ml[((slot0 + q) * G + g) * 2]);
-    // pass 2: weights against that max; loads carry no dependency on the math
-    float L = 0.f, A = 0.f;
-#pragma unroll 8
-    for (int q = wave; q < S; q += NW) {
-        const size_t sl = (slot0 + q) * G + g;
-        const float b = fast_exp2(p.ws_ml[sl * 2] - M);
-        L += p.ws_ml[sl * 2 + 1] * b;
-        A += p.ws_acc[sl * D + d] * b;
+    // One pass: batches of CB splits are loaded together (no load depends on
+    // the math) and merged into a running (M, L, A) with online rescaling.
+    constexpr int CB = 8;
+    float M = NEG_BIG, L = 0.f, A = 0.f;
+    for (int q0 = wave; q0 < S; q0 += NW * CB) {
+        float mq[CB], lq[CB], aq[CB];
+#pragma unroll
+        for (int u = 0; u < CB; u++) {
+            const int q = q0 + u * NW;
+            const size_t sl = (slot0 + (q < S ? q : q0)) * G + g;
+            mq[u] = q < S ? p.ws_ml[sl * 2] : NEG_BIG;
+            lq[u] = p.ws_ml[sl * 2 + 1];
+            aq[u] = p.ws_acc[sl * D + d];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int u = 0; u < CB; u++) Mn = fmaxf(Mn, mq[u]);
+        const float r = fast_exp2(M - Mn);
+        L *= r;
+        A *= r;
+#pragma unroll
+        for (int u = 0; u < CB; u++) {
+            const float b = (q0 + u * NW < S) ? fast_exp2(mq[u] - Mn) : 0.f;
+            L += lq[u] * b;
+            A += aq[u] * b;
+        }
+        M = Mn;
     }
     s_a[wave][lane] = A;
     if (lane == 0) {
@@ -391,8 +407,10 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
 template <int G, bool FUSED>
 hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
     dim3 grid(a->n_splits, a->n_kv_heads);
+    if (a->ev0 && hipEventRecord((hipEvent_t)a->ev0, st) != hipSuccess) return hipErrorInvalidValue;
     hipLaunchKernelGGL((decode_kernel<G, FUSED>), grid, dim3(NT), 0, st, *a);
     hipError_t e = hipGetLastError();
+    if (a->ev1 && hipEventRecord((hipEvent_t)a->ev1, st) != hipSuccess) return hipErrorInvalidValue;
     if (e != hipSuccess || a->n_splits == 1) return e;
     hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 64, G, a->n_kv_heads), dim3(NT), 0, st, *a);
     return hipGetLastError();

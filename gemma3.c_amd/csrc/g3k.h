@@ -48,6 +48,7 @@ typedef struct {
     float *out;            /* [H_q][D] */
     float *ws_acc;         /* [H_kv][G3K_MAX_SPLITS][group][D] split partials */
     float *ws_ml;          /* [H_kv][G3K_MAX_SPLITS][group][2] (max, sum) */
+    void *ev0, *ev1;       /* hipEvent_t recorded around decode_kernel, or NULL */
 } g3k_decode_args;
 
 /* QK-norm + RoPE of q (and of the new k), cache write of the new k/v and
@@ -74,9 +75,53 @@ typedef struct {
     long long dst_head_stride;
     int ring;              /* >0: slot = pos % ring; 0: slot = pos - dst_pos0 */
     int dst_pos0;
+    int kv_skip;           /* tokens i < kv_skip are not written to k_dst / v_dst */
+    /* optional prefill staging of the rotated keys, fp16 hi / lo parts
+     * (bit patterns), [n_kv_heads][ldk][D], token i at row row0 + i */
+    uint16_t *k_hi, *k_lo;
+    long long ldk;
+    int row0;
 } g3k_rope_write_args;
 
 int g3k_rope_write(const g3k_rope_write_args *a, void *stream);
+
+/* Prefill staging of key rows kk0..kk0+cnt-1 (key index kk = position -
+ * kstart): K (already normed + rotated, fp32) -> fp16 hi / lo rows of
+ * k_hi / k_lo [H_kv][ldk][D]; V (fp32) -> bf16 columns of vt [H_kv][D][ldk].
+ * Source row of key kk (position pos = kstart + kk) for head h:
+ *   src + h*head_stride + r*row_stride, r = ring ? pos % ring : pos - row_pos0.
+ * k_src == NULL stages V only.  Key indices in [nk, kk0+cnt) are written as
+ * zeros (K rows and V columns) without reading the source. */
+typedef struct {
+    const float *k_src, *v_src;
+    long long head_stride, row_stride;
+    int ring, row_pos0, kstart;
+    int kk0, cnt, nk, n_kv_heads;
+    uint16_t *k_hi, *k_lo, *vt;
+    long long ldk;
+} g3k_stage_args;
+
+int g3k_stage(const g3k_stage_args *a, void *stream);
+
+/* Causal / sliding-window prefill attention on MFMA (one launch).
+ *   q:  normed + rotated queries, fp32 head-major [H_q][n][D]; token i has
+ *       key index hist + i.
+ *   k_hi / k_lo: fp16 split keys [H_kv][ldk][D]; vt: bf16 values [H_kv][D][ldk],
+ *       nk valid key indices, zero padded to ldk (a multiple of 64).
+ *   Query i attends key indices kk with hist+i-window < kk <= hist+i.
+ *   out: [n][H_q][D] fp32 (the reference's attn_out layout). */
+typedef struct {
+    const float *q;
+    const uint16_t *k_hi, *k_lo, *vt;
+    float *out;
+    long long ldk;
+    int n, hist, nk, window;  /* window: INT_MAX / 2 for global layers */
+    int n_kv_heads, group;
+    float qscale;             /* softmax scale * log2(e) */
+    void *ev0, *ev1;          /* hipEvent_t recorded around prefill_kernel, or NULL */
+} g3k_prefill_args;
+
+int g3k_prefill(const g3k_prefill_args *a, void *stream);
 
 #ifdef __cplusplus
 }

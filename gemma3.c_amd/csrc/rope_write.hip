@@ -6,7 +6,10 @@
 // (gemma3_transformer.c:236-251), for every token of a batch in one launch.
 // Q heads go to a head-major [H_q][n][D] buffer for the prefill attention
 // kernel; K (normed + RoPE'd) and V rows go to the cache (or to a staging
-// buffer), head-major [H_kv][rows][D].
+// buffer), head-major [H_kv][rows][D].  For prefill the rotated keys are also
+// written as fp16 hi / lo parts to the attention kernel's staging rows, and
+// tokens whose ring slot a later token of the same batch overwrites
+// (kv_skip) are not written to the cache.
 //
 // One wave per 256-float head vector.  Lane l holds dims {2l, 2l+1} and their
 // RoPE partners {2l+128, 2l+129}: two 512-byte coalesced float2 loads, the
@@ -20,6 +23,10 @@ namespace {
 
 using namespace g3k;
 constexpr int D = G3K_HEAD_DIM;
+
+__device__ __forceinline__ uint32_t pack_f16(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | (uint32_t)__builtin_bit_cast(uint16_t, b) << 16;
+}
 
 __global__ __launch_bounds__(256) void rope_write_kernel(g3k_rope_write_args a) {
     const int nq = a.Q ? a.n_heads : 0;
@@ -67,6 +74,19 @@ __global__ __launch_bounds__(256) void rope_write_kernel(g3k_rope_write_args a) 
         lo.y = a1 * t.z - b1 * t.w;
         hi.y = a1 * t.w + b1 * t.z;
     }
+
+    if (kind == 1 && a.k_hi) {
+        // prefill staging: fp16 hi / lo split of the rotated key
+        const _Float16 h0 = (_Float16)lo.x, h1 = (_Float16)lo.y, h2 = (_Float16)hi.x, h3 = (_Float16)hi.y;
+        const _Float16 l0 = (_Float16)(lo.x - (float)h0), l1 = (_Float16)(lo.y - (float)h1);
+        const _Float16 l2 = (_Float16)(hi.x - (float)h2), l3 = (_Float16)(hi.y - (float)h3);
+        const size_t o = ((size_t)h * a.ldk + a.row0 + i) * D;
+        *reinterpret_cast<uint32_t *>(a.k_hi + o + 2 * lane) = pack_f16(h0, h1);
+        *reinterpret_cast<uint32_t *>(a.k_hi + o + 128 + 2 * lane) = pack_f16(h2, h3);
+        *reinterpret_cast<uint32_t *>(a.k_lo + o + 2 * lane) = pack_f16(l0, l1);
+        *reinterpret_cast<uint32_t *>(a.k_lo + o + 128 + 2 * lane) = pack_f16(l2, l3);
+    }
+    if (kind != 0 && i < a.kv_skip) return;
 
     float *dst;
     if (kind == 0) {

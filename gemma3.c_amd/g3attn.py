@@ -91,9 +91,12 @@ def lib():
     L.g3attn_stream.restype = _vp
     L.g3attn_synchronize.argtypes = [_vp]
     L.g3attn_last_error.restype = C.c_char_p
+    L.g3attn_profile_enable.argtypes = [_vp, C.c_int]
+    L.g3attn_profile_read.argtypes = [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
-                 "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize"):
+                 "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
+                 "g3attn_profile_enable", "g3attn_profile_read"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -203,6 +206,17 @@ class Context:
 
     def synchronize(self):
         _check(lib().g3attn_synchronize(self._h))
+
+    def profile(self, enable: bool = True):
+        """Bracket the main attention kernel of every call with HIP events."""
+        _check(lib().g3attn_profile_enable(self._h, int(enable)))
+
+    def profile_read(self, kind: int):
+        """(summed ms, launches) of kind 0 (decode kernel) or 1 (prefill kernel) since the
+        last read."""
+        ms, n = C.c_double(), C.c_int()
+        _check(lib().g3attn_profile_read(self._h, kind, C.byref(ms), C.byref(n)))
+        return ms.value, n.value
 
     def decode(self, layer, pos, q, k, v, q_norm=None, k_norm=None) -> np.ndarray:
         out = np.empty(self.qs, dtype=np.float32)

@@ -25,6 +25,7 @@
 #define G3_ERR_CONTEXT_OVERFLOW (-8)
 
 #define LOG2E 1.4426950408889634f
+#define G3_PROF_CAP 256
 #define D G3K_HEAD_DIM
 
 /* ------------------------------------------------------------------ errors */
@@ -104,12 +105,36 @@ struct g3attn_ctx {
     /* grow-on-demand device buffers for host-pointer batch calls */
     void *d_big;
     size_t d_big_cap;
+    /* grow-on-demand prefill workspace (staged queries and keys) */
+    void *d_pf;
+    size_t d_pf_cap;
+    /* kernel timing (g3attn_profile_*): event pairs per kind */
+    struct {
+        int on;
+        hipEvent_t ev[2][G3_PROF_CAP][2];
+        int used[2];
+        double ms[2];
+        int count[2];
+    } prof;
     int split_rows; /* 0 = heuristic */
+    int min_rows;   /* smallest heuristic split */
     int target_wgs; /* decode workgroups per call (all KV heads) */
 };
 
+static void prof_destroy(g3attn_ctx *c) {
+    for (int k = 0; k < 2; k++)
+        for (int i = 0; i < G3_PROF_CAP; i++)
+            for (int j = 0; j < 2; j++)
+                if (c->prof.ev[k][i][j]) {
+                    hipEventDestroy(c->prof.ev[k][i][j]);
+                    c->prof.ev[k][i][j] = NULL;
+                }
+    c->prof.on = 0;
+}
+
 static void ctx_free(g3attn_ctx *c) {
     if (!c) return;
+    prof_destroy(c);
     if (c->kc)
         for (int l = 0; l < c->cfg.num_layers; l++) hipFree(c->kc[l]);
     if (c->vc)
@@ -124,6 +149,7 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_in);
     hipFree(c->d_out);
     hipFree(c->d_big);
+    hipFree(c->d_pf);
     if (c->h_in) hipHostFree(c->h_in);
     if (c->h_out) hipHostFree(c->h_out);
     if (c->stream) hipStreamDestroy(c->stream);
@@ -205,9 +231,12 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
     if (!alloc_dev((void **)&c->ws_ml, slots * 2 * sizeof(float), "decode workspace")) goto fail;
     {
         const char *w = getenv("G3ATTN_DECODE_WGS");
+        const char *mr = getenv("G3ATTN_SPLIT_MIN_ROWS");
         int cus = 0;
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device);
-        c->target_wgs = w ? atoi(w) : (cus > 0 ? cus : 256);
+        c->target_wgs = w ? atoi(w) : 2 * (cus > 0 ? cus : 256);
+        c->min_rows = mr ? atoi(mr) : 64;
+        if (c->min_rows < 64) c->min_rows = 64;
     }
 
     const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D;
@@ -262,22 +291,100 @@ static int grow_big(g3attn_ctx *c, size_t bytes) {
     return G3_OK;
 }
 
+/* ------------------------------------------------------------------ timing */
+
+/* Folds the recorded pairs of one kind into its running sum. */
+static int prof_fold(g3attn_ctx *c, int kind) {
+    if (!c->prof.used[kind]) return G3_OK;
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_profile");
+    for (int i = 0; i < c->prof.used[kind]; i++) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, c->prof.ev[kind][i][0], c->prof.ev[kind][i][1]),
+                "g3attn_profile");
+        c->prof.ms[kind] += ms;
+    }
+    c->prof.count[kind] += c->prof.used[kind];
+    c->prof.used[kind] = 0;
+    return G3_OK;
+}
+
+/* Event pair for the next launch of `kind` (both NULL when timing is off). */
+static int prof_slot(g3attn_ctx *c, int kind, void **ev0, void **ev1) {
+    *ev0 = *ev1 = NULL;
+    if (!c->prof.on) return G3_OK;
+    if (c->prof.used[kind] == G3_PROF_CAP) {
+        int rc = prof_fold(c, kind);
+        if (rc) return rc;
+    }
+    const int i = c->prof.used[kind]++;
+    *ev0 = c->prof.ev[kind][i][0];
+    *ev1 = c->prof.ev[kind][i][1];
+    return G3_OK;
+}
+
+int g3attn_profile_enable(g3attn_ctx *c, int enable) {
+    if (!c) {
+        set_err("g3attn_profile_enable: null context");
+        return G3_ERR_INVALID_ARG;
+    }
+    hipSetDevice(c->device);
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_profile_enable");
+    if (!enable) {
+        prof_destroy(c);
+        return G3_OK;
+    }
+    if (c->prof.on) return G3_OK;
+    for (int k = 0; k < 2; k++) {
+        c->prof.used[k] = c->prof.count[k] = 0;
+        c->prof.ms[k] = 0.0;
+        for (int i = 0; i < G3_PROF_CAP; i++)
+            for (int j = 0; j < 2; j++) {
+                hipError_t e = hipEventCreate(&c->prof.ev[k][i][j]);
+                if (e != hipSuccess) {
+                    prof_destroy(c);
+                    return hip_fail(e, "g3attn_profile_enable");
+                }
+            }
+    }
+    c->prof.on = 1;
+    return G3_OK;
+}
+
+int g3attn_profile_read(g3attn_ctx *c, int kind, double *total_ms, int *count) {
+    if (!c || kind < 0 || kind > 1 || !total_ms || !count) {
+        set_err("g3attn_profile_read: bad arguments");
+        return G3_ERR_INVALID_ARG;
+    }
+    *total_ms = 0.0;
+    *count = 0;
+    if (!c->prof.on) return G3_OK;
+    hipSetDevice(c->device);
+    int rc = prof_fold(c, kind);
+    if (rc) return rc;
+    *total_ms = c->prof.ms[kind];
+    *count = c->prof.count[kind];
+    c->prof.ms[kind] = 0.0;
+    c->prof.count[kind] = 0;
+    return G3_OK;
+}
+
 /* ------------------------------------------------------------------ decode */
 
-/* Split-K shape: about one resident wave of workgroups (capacity =
- * occupancy x CUs, G3ATTN_DECODE_WGS overrides) spread over the KV heads, at
- * least 256 rows per workgroup, at most G3K_MAX_SPLITS splits per head. */
+/* Split-K shape: target_wgs workgroups (default two per compute unit,
+ * G3ATTN_DECODE_WGS overrides) spread over the KV heads, rows per split a
+ * multiple of 64 and at least min_rows (G3ATTN_SPLIT_MIN_ROWS, default 64),
+ * at most G3K_MAX_SPLITS splits per head. */
 static void choose_splits(int n_stream, int n_kv, int target_wgs, int override_rows,
-                          g3k_decode_args *a) {
+                          int min_rows, g3k_decode_args *a) {
     if (n_stream <= 0) {
         a->rows_per_split = 64;
         a->n_splits = 1;
         return;
     }
-    long per_head = (target_wgs > 0 ? target_wgs : 256) / n_kv;
+    long per_head = (target_wgs > 0 ? target_wgs : 512) / n_kv;
     if (per_head < 1) per_head = 1;
     long r = override_rows > 0 ? override_rows : (n_stream + per_head - 1) / per_head;
-    if (override_rows <= 0 && r < 256) r = 256;
+    if (override_rows <= 0 && r < min_rows) r = min_rows;
     r = (r + 63) / 64 * 64;
     long s = (n_stream + r - 1) / r;
     if (s > G3K_MAX_SPLITS) {
@@ -337,14 +444,16 @@ int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, cons
     a.new_slot = slot;
     a.mask = NULL;
     a.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
-    choose_splits(a.n_stream, c->cfg.num_kv_heads, c->target_wgs, c->split_rows, &a);
+    choose_splits(a.n_stream, c->cfg.num_kv_heads, c->target_wgs, c->split_rows, c->min_rows, &a);
     a.n_kv_heads = c->cfg.num_kv_heads;
     a.group = c->group;
     a.out = attn_out;
     a.ws_acc = c->ws_acc;
     a.ws_ml = c->ws_ml;
     hipSetDevice(c->device);
-    const int rc = g3k_decode(&a, 1, c->stream);
+    int rc = prof_slot(c, 0, &a.ev0, &a.ev1);
+    if (rc) return rc;
+    rc = g3k_decode(&a, 1, c->stream);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_decode launch");
     return G3_OK;
 }
@@ -495,19 +604,195 @@ int g3attn_kv_read(g3attn_ctx *c, int layer, int slot, int n, float *k_rows, flo
 
 /* ------------------------------------------------------------------ prefill */
 
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+/* Grow-on-demand prefill workspace: q_out [H_q][n][D] fp32, k_hi / k_lo
+ * [H_kv][ldk][D] fp16 and vt [H_kv][D][ldk] bf16. */
+static int grow_pf(g3attn_ctx *c, size_t bytes) {
+    if (bytes <= c->d_pf_cap) return G3_OK;
+    HIP_TRY(hipStreamSynchronize(c->stream), "grow prefill workspace");
+    hipFree(c->d_pf);
+    c->d_pf = NULL;
+    c->d_pf_cap = 0;
+    if (!alloc_dev(&c->d_pf, bytes, "prefill workspace")) return G3_ERR_OUT_OF_MEMORY;
+    c->d_pf_cap = bytes;
+    return G3_OK;
+}
+
 int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
                           const float *K, const float *V, const uint16_t *q_norm,
                           const uint16_t *k_norm, float *attn_out) {
-    (void)start_pos; (void)n; (void)Q; (void)K; (void)V; (void)q_norm; (void)k_norm; (void)attn_out;
     if (!check_layer(c, layer, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
-    set_err("g3attn_prefill: not available in this build");
-    return G3_ERR_INVALID_ARG;
+    if (n < 0 || start_pos < 0 || (n > 0 && (!Q || !K || !V || !attn_out))) {
+        set_err("g3attn_prefill: null buffer or negative start_pos / n");
+        return G3_ERR_INVALID_ARG;
+    }
+    if ((long)start_pos + n > c->max_context) {
+        set_err("g3attn_prefill: positions up to %ld exceed max_context %d",
+                (long)start_pos + n - 1, c->max_context);
+        return G3_ERR_CONTEXT_OVERFLOW;
+    }
+    if (n == 0) return G3_OK;
+    const int is_global = g3attn_is_global_layer(layer);
+    const int W = c->cfg.sliding_window;
+    const int Hq = c->cfg.num_heads, Hkv = c->cfg.num_kv_heads;
+    /* Keys the batch can see: positions [kstart, start_pos + n), staged in
+     * position order (key index kk = pos - kstart); the first hist of them
+     * come from the cache, written by earlier calls. */
+    const int kstart = is_global ? 0 : (start_pos - W + 1 > 0 ? start_pos - W + 1 : 0);
+    const int hist = start_pos - kstart, nk = hist + n;
+    const long long ldk = ((long long)nk + 63) / 64 * 64;
+    const size_t q_bytes = align256((size_t)n * Hq * D * sizeof(float));
+    const size_t k_bytes = align256((size_t)Hkv * ldk * D * sizeof(uint16_t));
+    hipSetDevice(c->device);
+    int rc = grow_pf(c, q_bytes + 3 * k_bytes);
+    if (rc) return rc;
+    unsigned char *ws = (unsigned char *)c->d_pf;
+    float *q_out = (float *)ws;
+    uint16_t *k_hi = (uint16_t *)(ws + q_bytes);
+    uint16_t *k_lo = (uint16_t *)(ws + q_bytes + k_bytes);
+    uint16_t *vt = (uint16_t *)(ws + q_bytes + 2 * k_bytes);
+    const long long head_stride = (long long)c->rows[layer] * D;
+
+    /* 1. history keys, read from the cache before this batch's ring writes */
+    if (hist > 0) {
+        g3k_stage_args sa;
+        memset(&sa, 0, sizeof sa);
+        sa.k_src = c->kc[layer];
+        sa.v_src = c->vc[layer];
+        sa.head_stride = head_stride;
+        sa.row_stride = D;
+        sa.ring = is_global ? 0 : W;
+        sa.row_pos0 = 0;
+        sa.kstart = kstart;
+        sa.kk0 = 0;
+        sa.cnt = hist;
+        sa.nk = nk;
+        sa.n_kv_heads = Hkv;
+        sa.k_hi = k_hi;
+        sa.k_lo = k_lo;
+        sa.vt = vt;
+        sa.ldk = ldk;
+        rc = g3k_stage(&sa, c->stream);
+        if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill stage");
+    }
+    /* 2. QK-norm + RoPE of the batch, cache_kv, fp16 split keys
+     *    (gemma3_transformer.c:650-671 for every token) */
+    g3k_rope_write_args ra;
+    memset(&ra, 0, sizeof ra);
+    ra.Q = Q;
+    ra.K = K;
+    ra.V = V;
+    ra.q_norm = (q_norm && k_norm) ? q_norm : NULL;
+    ra.k_norm = (q_norm && k_norm) ? k_norm : NULL;
+    ra.rope = is_global ? c->rope_global : c->rope_local;
+    ra.eps = c->cfg.rmsnorm_eps;
+    ra.n = n;
+    ra.start_pos = start_pos;
+    ra.n_heads = Hq;
+    ra.n_kv_heads = Hkv;
+    ra.q_out = q_out;
+    ra.k_dst = c->kc[layer];
+    ra.v_dst = c->vc[layer];
+    ra.dst_head_stride = head_stride;
+    ra.ring = is_global ? 0 : W;
+    ra.dst_pos0 = 0;
+    ra.kv_skip = (!is_global && n > W) ? n - W : 0;
+    ra.k_hi = k_hi;
+    ra.k_lo = k_lo;
+    ra.ldk = ldk;
+    ra.row0 = hist;
+    rc = g3k_rope_write(&ra, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill rope");
+    /* 3. the batch's values as bf16 V^T, and zeroed padding up to ldk */
+    {
+        g3k_stage_args sa;
+        memset(&sa, 0, sizeof sa);
+        sa.k_src = NULL;
+        sa.v_src = V;
+        sa.head_stride = D;
+        sa.row_stride = (long long)Hkv * D;
+        sa.ring = 0;
+        sa.row_pos0 = start_pos;
+        sa.kstart = kstart;
+        sa.kk0 = hist;
+        sa.cnt = (int)(ldk - hist);
+        sa.nk = nk;
+        sa.n_kv_heads = Hkv;
+        sa.k_hi = k_hi;
+        sa.k_lo = k_lo;
+        sa.vt = vt;
+        sa.ldk = ldk;
+        rc = g3k_stage(&sa, c->stream);
+        if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill stage");
+    }
+    /* 4. attention (gemma3_gqa for every token, gemma3_transformer.c:673-691) */
+    g3k_prefill_args pa;
+    memset(&pa, 0, sizeof pa);
+    pa.q = q_out;
+    pa.k_hi = k_hi;
+    pa.k_lo = k_lo;
+    pa.vt = vt;
+    pa.out = attn_out;
+    pa.ldk = ldk;
+    pa.n = n;
+    pa.hist = hist;
+    pa.nk = nk;
+    pa.window = is_global ? INT_MAX / 2 : W;
+    pa.n_kv_heads = Hkv;
+    pa.group = c->group;
+    pa.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
+    rc = prof_slot(c, 1, &pa.ev0, &pa.ev1);
+    if (rc) return rc;
+    rc = g3k_prefill(&pa, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill launch");
+    return G3_OK;
 }
 
 int g3attn_prefill(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
                    const float *K, const float *V, const uint16_t *q_norm,
                    const uint16_t *k_norm, float *attn_out) {
-    return g3attn_prefill_device(c, layer, start_pos, n, Q, K, V, q_norm, k_norm, attn_out);
+    if (!check_layer(c, layer, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
+    if (n < 0 || (n > 0 && (!Q || !K || !V || !attn_out))) {
+        set_err("g3attn_prefill: null buffer or n < 0");
+        return G3_ERR_INVALID_ARG;
+    }
+    if (start_pos < 0) {
+        set_err("g3attn_prefill: start_pos < 0");
+        return G3_ERR_INVALID_ARG;
+    }
+    if ((long)start_pos + n > c->max_context) {
+        set_err("g3attn_prefill: positions up to %ld exceed max_context %d",
+                (long)start_pos + n - 1, c->max_context);
+        return G3_ERR_CONTEXT_OVERFLOW;
+    }
+    if (n == 0) return G3_OK;
+    const size_t qb = align256((size_t)n * c->cfg.num_heads * D * sizeof(float));
+    const size_t kb = align256((size_t)n * c->cfg.num_kv_heads * D * sizeof(float));
+    const int norm = q_norm && k_norm;
+    hipSetDevice(c->device);
+    int rc = grow_big(c, 2 * qb + 2 * kb + 2 * align256(D * sizeof(uint16_t)));
+    if (rc) return rc;
+    unsigned char *b = (unsigned char *)c->d_big;
+    float *dQ = (float *)b, *dO = (float *)(b + qb);
+    float *dK = (float *)(b + 2 * qb), *dV = (float *)(b + 2 * qb + kb);
+    uint16_t *dqn = (uint16_t *)(b + 2 * qb + 2 * kb);
+    uint16_t *dkn = dqn + D;
+    const size_t qs = (size_t)n * c->cfg.num_heads * D * sizeof(float);
+    const size_t ks = (size_t)n * c->cfg.num_kv_heads * D * sizeof(float);
+    HIP_TRY(hipMemcpyAsync(dQ, Q, qs, hipMemcpyHostToDevice, c->stream), "prefill upload");
+    HIP_TRY(hipMemcpyAsync(dK, K, ks, hipMemcpyHostToDevice, c->stream), "prefill upload");
+    HIP_TRY(hipMemcpyAsync(dV, V, ks, hipMemcpyHostToDevice, c->stream), "prefill upload");
+    if (norm) {
+        HIP_TRY(hipMemcpyAsync(dqn, q_norm, D * 2, hipMemcpyHostToDevice, c->stream), "prefill upload");
+        HIP_TRY(hipMemcpyAsync(dkn, k_norm, D * 2, hipMemcpyHostToDevice, c->stream), "prefill upload");
+    }
+    rc = g3attn_prefill_device(c, layer, start_pos, n, dQ, dK, dV, norm ? dqn : NULL,
+                               norm ? dkn : NULL, dO);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(attn_out, dO, qs, hipMemcpyDeviceToHost, c->stream), "prefill download");
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_prefill");
+    return G3_OK;
 }
 
 /* ------------------------------------------------------------------ gemma3_gqa */
@@ -580,7 +865,7 @@ static int gqa_run(float *output, const float *q, const float *k_cache, const fl
     a.new_slot = -1;
     a.mask = dm;
     a.qscale = scale * LOG2E;
-    choose_splits(seq_len, n_kv, 256, 0, &a);
+    choose_splits(seq_len, n_kv, 512, 0, 64, &a);
     a.n_kv_heads = n_kv;
     a.group = n_heads / n_kv;
     a.out = dout;

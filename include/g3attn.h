@@ -149,6 +149,16 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
 void *g3attn_stream(g3attn_ctx *ctx);
 int g3attn_synchronize(g3attn_ctx *ctx);
 
+/* Kernel timing for benchmarks (no counterpart in the reference, which has no
+ * timers).  While enabled, every decode / prefill call brackets its main
+ * attention kernel (kind 0: the split-K decode kernel, without the split
+ * combine; kind 1: the prefill MFMA kernel, without the staging kernels)
+ * with HIP events on the context stream.  g3attn_profile_read waits for the
+ * stream and returns, for one kind, the launches bracketed since the last
+ * read and their summed duration in milliseconds, then resets that kind. */
+int g3attn_profile_enable(g3attn_ctx *ctx, int enable);
+int g3attn_profile_read(g3attn_ctx *ctx, int kind, double *total_ms, int *count);
+
 /* Thread-local message of the last failure on this thread ("" if none). */
 const char *g3attn_last_error(void);
 

@@ -239,7 +239,9 @@ typedef struct {
     const float *Kc, *Vc; /* [cache rows + n] combined: cache snapshot then batch rows */
     const g3o_config *cfg;
     int is_global, start_pos, n, cache_rows;
-    int next; /* work counter (under lock) */
+    const int *sel; /* tokens to compute (NULL: all n) */
+    int n_out;      /* number of output rows */
+    int next;       /* work counter (under lock) */
     pthread_mutex_t lock;
 } mt_job;
 
@@ -256,9 +258,10 @@ static void *mt_worker(void *arg) {
     if (!rows || !mask || !scores) goto done;
     for (;;) {
         pthread_mutex_lock(&J->lock);
-        const int i = J->next < J->n ? J->next++ : -1;
+        const int j = J->next < J->n_out ? J->next++ : -1;
         pthread_mutex_unlock(&J->lock);
-        if (i < 0) break;
+        if (j < 0) break;
+        const int i = J->sel ? J->sel[j] : j;
         const int pos = J->start_pos + i;
         const int seq_len = attn_seq_len(cfg, J->is_global, pos);
         for (int s = 0; s < seq_len; s++) {
@@ -266,7 +269,7 @@ static void *mt_worker(void *arg) {
             const int p = J->is_global ? s : pos - ((pos - s) % W);
             rows[s] = p >= J->start_pos ? J->cache_rows + (p - J->start_pos) : s;
         }
-        g3o_gqa_rows(J->attn_out + (size_t)i * qs, J->Q + (size_t)i * qs, J->Kc, J->Vc, rows,
+        g3o_gqa_rows(J->attn_out + (size_t)j * qs, J->Q + (size_t)i * qs, J->Kc, J->Vc, rows,
                      cfg->num_heads, cfg->num_kv_heads, seq_len, cfg->head_dim, scale, mask,
                      scores);
     }
@@ -281,7 +284,19 @@ int g3o_prefill_mt(float *attn_out, float *Q, float *K, const float *V,
                    const uint16_t *q_norm, const uint16_t *k_norm,
                    float *k_cache, float *v_cache, const float *rope,
                    const g3o_config *cfg, int layer, int start_pos, int n, int threads) {
-    if (start_pos < 0 || n < 0) return -1;
+    return g3o_prefill_rows(attn_out, Q, K, V, q_norm, k_norm, k_cache, v_cache, rope, cfg, layer,
+                            start_pos, n, NULL, n, threads);
+}
+
+int g3o_prefill_rows(float *attn_out, float *Q, float *K, const float *V,
+                     const uint16_t *q_norm, const uint16_t *k_norm,
+                     float *k_cache, float *v_cache, const float *rope,
+                     const g3o_config *cfg, int layer, int start_pos, int n,
+                     const int *sel, int n_sel, int threads) {
+    if (start_pos < 0 || n < 0 || n_sel < 0) return -1;
+    if (sel)
+        for (int j = 0; j < n_sel; j++)
+            if (sel[j] < 0 || sel[j] >= n) return -1;
     if (start_pos + n > cfg->max_context) return -8;
     if (n == 0) return 0;
     const int is_global = g3o_is_global_layer(layer);
@@ -315,6 +330,8 @@ int g3o_prefill_mt(float *attn_out, float *Q, float *K, const float *V,
     J.start_pos = start_pos;
     J.n = n;
     J.cache_rows = cache_rows;
+    J.sel = sel;
+    J.n_out = sel ? n_sel : n;
     J.next = 0;
     pthread_mutex_init(&J.lock, NULL);
     if (threads <= 0) threads = (int)sysconf(_SC_NPROCESSORS_ONLN);

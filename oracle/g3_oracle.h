@@ -18,6 +18,7 @@
  *   g3o_cache_kv                             gemma3_transformer.c:236-251
  *   g3o_layer_decode                         gemma3_transformer.c:294-352
  *   g3o_prefill                              gemma3_transformer.c:641-692
+ *   g3o_prefill_mt / g3o_prefill_rows        the same loop, tokens in parallel
  *   g3o_is_global_layer / g3o_layer_theta    gemma3.h:347-360
  *
  * How each function is pinned (tests/test_oracle_*.py):
@@ -111,6 +112,15 @@ int g3o_prefill_mt(float *attn_out, float *Q, float *K, const float *V,
                    const uint16_t *q_norm, const uint16_t *k_norm,
                    float *k_cache, float *v_cache, const float *rope,
                    const g3o_config *cfg, int layer, int start_pos, int n, int threads);
+
+/* g3o_prefill_mt restricted to the tokens sel[0..n_sel-1] (indices into the
+ * batch): attn_out [n_sel][H_q*d] row j is token sel[j].  Q/K are normed +
+ * RoPE'd in place and the cache ends in the same state as after g3o_prefill. */
+int g3o_prefill_rows(float *attn_out, float *Q, float *K, const float *V,
+                     const uint16_t *q_norm, const uint16_t *k_norm,
+                     float *k_cache, float *v_cache, const float *rope,
+                     const g3o_config *cfg, int layer, int start_pos, int n,
+                     const int *sel, int n_sel, int threads);
 
 /* QK-norm + RoPE of n tokens x n_heads vectors in place (X [n][n_heads][d]),
  * token i at position start_pos + i: the same per-vector calls as

@@ -99,6 +99,10 @@ def lib():
                                      _f32p, _f32p, C.POINTER(_Cfg), C.c_int, C.c_int, C.c_int,
                                      C.c_int]
         L.g3o_prefill_mt.restype = C.c_int
+        L.g3o_prefill_rows.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _f32p,
+                                       _f32p, _f32p, C.POINTER(_Cfg), C.c_int, C.c_int, C.c_int,
+                                       _i32p, C.c_int, C.c_int]
+        L.g3o_prefill_rows.restype = C.c_int
         L.g3o_norm_rope_batch.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_void_p, _f32p,
                                           C.c_int, C.c_float, C.c_int]
         L.g3o_gen_normal_bf16.argtypes = [_f32p, C.c_size_t, C.c_uint64, C.c_size_t, C.c_int]
@@ -261,6 +265,23 @@ def prefill(cfg: Config, layer: int, start_pos: int, Q, K, V, k_cache, v_cache, 
     if rc:
         raise RuntimeError(f"g3o_prefill rc={rc}")
     return out, Q, K
+
+
+def prefill_rows(cfg: Config, layer: int, start_pos: int, Q, K, V, k_cache, v_cache, table,
+                 rows, q_norm=None, k_norm=None, threads: int = 0):
+    """Prefill (gemma3_transformer.c:641-692) evaluated only for batch tokens `rows`.
+    Returns attn_out [len(rows)][H_q*d]; k_cache / v_cache end as after the full loop."""
+    Q = np.array(Q, dtype=np.float32, copy=True)
+    K = np.array(K, dtype=np.float32, copy=True)
+    V = np.ascontiguousarray(V, dtype=np.float32)
+    sel = np.ascontiguousarray(rows, dtype=np.int32)
+    out = np.empty((sel.size, cfg.num_heads * cfg.head_dim), dtype=np.float32)
+    c = cfg.c()
+    rc = lib().g3o_prefill_rows(out, Q, K, V, _ptr(q_norm), _ptr(k_norm), k_cache, v_cache, table,
+                                C.byref(c), layer, start_pos, Q.shape[0], sel, sel.size, threads)
+    if rc:
+        raise RuntimeError(f"g3o_prefill_rows rc={rc}")
+    return out
 
 
 # ---------------------------------------------------------------- reference harness

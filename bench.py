@@ -64,6 +64,19 @@ def prefill_flops(n: int, window: int) -> float:
     return 4.0 * HQ * D * prefill_pairs(n, window)
 
 
+def measured_traffic(key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary
+    (profiles/traffic.json: FETCH_SIZE / WRITE_SIZE scaled by a copy of known
+    size); None when absent."""
+    try:
+        with open(os.path.join(REPO, "profiles", "traffic.json")) as f:
+            t = json.load(f)
+        e = t[key]
+        return round(e["fetch_kib"] * 1024 / t["fetch_scale"] + e["write_kib"] * 1024 / t["write_scale"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def load_binding():
     spec = importlib.util.spec_from_file_location("g3attn", os.path.join(REPO, "gemma3.c_amd", "g3attn.py"))
     mod = importlib.util.module_from_spec(spec)
@@ -113,27 +126,45 @@ class Bench:
         return qkv, zn
 
     def time_calls(self, stream_ctx, calls, steps, warmup):
-        """Run `calls[i % len]` for warmup + steps; events on the library stream.
-        Returns (region seconds, mean per-launch-group seconds)."""
+        """Run `calls[i % len]` for warmup + steps on the library stream.
+        Returns (region seconds, mean per-call seconds, host wall seconds): the
+        region is bracketed by two events only, so back-to-back calls run as an
+        engine would issue them; per-call times come from a second pass with an
+        event pair around every call."""
         torch = self.torch
         s = torch.cuda.ExternalStream(stream_ctx.stream())
         for i in range(warmup):
             calls[i % len(calls)]()
         stream_ctx.synchronize()
         torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(s)
+        for i in range(steps):
+            calls[(warmup + i) % len(calls)]()
+        e1.record(s)
+        stream_ctx.synchronize()
+        wall = time.perf_counter() - t0
+        region = e0.elapsed_time(e1) * 1e-3
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
         ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        t0 = time.perf_counter()
         for i in range(steps):
             starts[i].record(s)
             calls[(warmup + i) % len(calls)]()
             ends[i].record(s)
         stream_ctx.synchronize()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        region = starts[0].elapsed_time(ends[-1]) * 1e-3
         per = [a.elapsed_time(b) * 1e-3 for a, b in zip(starts, ends)]
         return region, float(np.mean(per)), wall
+
+    def kernel_time(self, ctx, calls, steps, kind):
+        """Mean duration of the library's main kernel (kind 0 decode, 1 prefill)
+        over `steps` calls, from the event pairs the library records around it."""
+        ctx.profile(True)
+        for i in range(steps):
+            calls[i % len(calls)]()
+        ms, n = ctx.profile_read(kind)
+        ctx.profile(False)
+        return ms * 1e-3 / max(n, 1)
 
     # ---------------------------------------------------------------- decode
     def decode_calls(self, targets, pos, qkv, zn, out):
@@ -199,7 +230,10 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extra sections to run")
+    ap.add_argument("--only", default="",
+                    help="comma list of sections to run (decode8k = the headline, local512, 128k, "
+                         "stack, prefill, prefill_local_N2048_w1024, prefill_global_N8192); "
+                         "default: all")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device-to-device copies of this many MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -232,41 +266,59 @@ def main():
     extra = {}
 
     # ---------------- headline: configs[1] global decode, L = 8192
-    L = 8192
-    log("[bench] filling 2 x 34-layer contexts, 10 global layers x 8192 positions")
-    ctxs = [B.context(L) for _ in range(2)]
-    targets = []
-    for ctx in ctxs:
-        for layer in (5, 11, 17, 23, 29):
-            B.fill_layer(ctx, layer, L - 1)
-            targets.append((ctx, layer))
+    value = ms_per_step = achieved = kernel_s = call_s = None
     qkv, zn = B.token_inputs()
     out = torch.empty(QS, device=B.dev, dtype=torch.float32)
-    calls = B.decode_calls(targets, L - 1, qkv, zn, out)
-    # all calls go to ctx streams; both contexts are timed through ctx 0's
-    # stream only if they share it, so time each context's calls separately
-    log(f"[bench] headline decode L={L}: warmup {args.warmup}, steps {args.steps}")
-    per_ctx = []
-    for ci, ctx in enumerate(ctxs):
-        cl = [c for c, (cx, _) in zip(calls, targets) if cx is ctx]
-        for i in range(args.warmup):
-            cl[i % len(cl)]()
-        ctx.profile(True)
-        region, per_call, wall = B.time_calls(ctx, cl, args.steps, 0)
-        kms, kn = ctx.profile_read(0)
-        ctx.profile(False)
-        per_ctx.append((region, per_call, kms * 1e-3 / max(kn, 1)))
-    region = float(np.mean([r for r, _, _ in per_ctx]))
-    call_s = float(np.mean([c for _, c, _ in per_ctx]))
-    kernel_s = float(np.mean([k for _, _, k in per_ctx]))
-    ms_per_step = region / args.steps * 1e3
-    value = decode_bytes(L) / (region / args.steps) / 1e9
-    achieved = decode_bytes(L) / kernel_s / 1e9
-    log(f"[bench] headline: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s; call {call_s * 1e6:.2f} us; "
-        f"decode_kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
-    for c in ctxs:
-        c.close()
-    del ctxs, targets, calls
+    if not only or "decode8k" in only:
+        L = 8192
+        log("[bench] filling 2 x 34-layer contexts, 10 global layers x 8192 positions")
+        ctxs = [B.context(L) for _ in range(2)]
+        targets = []
+        for ctx in ctxs:
+            for layer in (5, 11, 17, 23, 29):
+                B.fill_layer(ctx, layer, L - 1)
+                targets.append((ctx, layer))
+        calls = B.decode_calls(targets, L - 1, qkv, zn, out)
+        # all calls go to ctx streams; both contexts are timed through ctx 0's
+        # stream only if they share it, so time each context's calls separately
+        log(f"[bench] headline decode L={L}: warmup {args.warmup}, steps {args.steps}")
+        per_ctx = []
+        for ci, ctx in enumerate(ctxs):
+            cl = [c for c, (cx, _) in zip(calls, targets) if cx is ctx]
+            region, per_call, wall = B.time_calls(ctx, cl, args.steps, args.warmup)
+            per_ctx.append((region, per_call, B.kernel_time(ctx, cl, args.steps, 0)))
+        region = float(np.mean([r for r, _, _ in per_ctx]))
+        call_s = float(np.mean([c for _, c, _ in per_ctx]))
+        kernel_s = float(np.mean([k for _, _, k in per_ctx]))
+        ms_per_step = region / args.steps * 1e3
+        value = decode_bytes(L) / (region / args.steps) / 1e9
+        achieved = decode_bytes(L) / kernel_s / 1e9
+        log(f"[bench] headline: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s; call {call_s * 1e6:.2f} us; "
+            f"decode_kernel {kernel_s * 1e6:.2f} us -> {achieved:.1f} GB/s")
+        for c in ctxs:
+            c.close()
+        del ctxs, targets, calls
+
+    # ---------------- configs[1] through the host-pointer entry point (PCIe-inclusive)
+    if not only or "decode8k_host" in only:
+        ctx = B.context(8192)
+        B.fill_layer(ctx, 5, 8191)
+        hq = [np.ascontiguousarray(t.cpu().numpy()) for t in qkv[0]]
+        hz = np.zeros(D, np.uint16)
+        for _ in range(20):
+            ctx.decode(5, 8191, hq[0], hq[1], hq[2], hz, hz)
+        ts = []
+        for _ in range(200):
+            t0 = time.perf_counter()
+            ctx.decode(5, 8191, hq[0], hq[1], hq[2], hz, hz)
+            ts.append(time.perf_counter() - t0)
+        extra["decode_global_L8192_host_pointers"] = {
+            "config": "configs[1] through g3attn_decode (host q/k/v in, host attn_out out, blocking)",
+            "us_per_call_median": round(float(np.median(ts)) * 1e6, 2),
+            "note": "one 64 MiB cache (LLC-warm); adds 16 KiB up + 8 KiB down over PCIe and a host sync",
+        }
+        log(f"[bench] decode8k host pointers: {extra['decode_global_L8192_host_pointers']}")
+        ctx.close()
 
     # ---------------- local decode at pos 511 (L = 512)
     if not only or "local512" in only:
@@ -276,10 +328,12 @@ def main():
             B.fill_layer(ctx, l, 511)
         cl = B.decode_calls([(ctx, l) for l in locs], 511, qkv, zn, out)
         region, per, _ = B.time_calls(ctx, cl, 200, 20)
+        ks = B.kernel_time(ctx, cl, 200, 0)
         extra["decode_local_L512"] = {
             "config": "configs[0]: local layer, pos 511, L=512, theta 1e4",
             "us_per_call": round(region / 200 * 1e6, 2),
-            "kernel_us": round(per * 1e6, 2),
+            "call_us": round(per * 1e6, 2),
+            "kernel_us": round(ks * 1e6, 2),
             "GB/s": round(decode_bytes(512) / (region / 200) / 1e9, 1),
             "bytes_per_call": decode_bytes(512),
         }
@@ -300,13 +354,15 @@ def main():
         pos = L - 1
         cl = B.decode_calls([(ctx, l) for l in glob], pos, qkv, zn, out)
         region, per, _ = B.time_calls(ctx, cl, 60, 6)
+        ks = B.kernel_time(ctx, cl, 60, 0)
         extra["decode_global_L131072"] = {
             "config": "global layer, pos 131071, L=131072, theta 1e6; 6 distinct 1 GiB caches rotated",
             "us_per_call": round(region / 60 * 1e6, 2),
-            "kernel_us": round(per * 1e6, 2),
+            "call_us": round(per * 1e6, 2),
+            "kernel_us": round(ks * 1e6, 2),
             "GB/s": round(decode_bytes(L) / (region / 60) / 1e9, 1),
-            "kernel_GB/s": round(decode_bytes(L) / per / 1e9, 1),
-            "frac_of_hbm_peak": round(decode_bytes(L) / per / 1e9 / HBM_PEAK_GBS, 4),
+            "kernel_GB/s": round(decode_bytes(L) / ks / 1e9, 1),
+            "frac_of_hbm_peak": round(decode_bytes(L) / ks / 1e9 / HBM_PEAK_GBS, 4),
             "bytes_per_call": decode_bytes(L),
         }
         log(f"[bench] 128k: {extra['decode_global_L131072']}")
@@ -345,14 +401,9 @@ def main():
         def pf(ctx=ctx, layer=layer, n=n, Q=Q, K=K, V=V, zn16=zn16, pout=pout):
             ctx.prefill_device(layer, 0, n, Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                zn16.data_ptr(), zn16.data_ptr(), pout.data_ptr())
-        for _ in range(3):
-            pf()
-        ctx.profile(True)
-        region, per_call, _ = B.time_calls(ctx, [pf], steps, 0)
-        kms, kn = ctx.profile_read(1)
-        ctx.profile(False)
+        region, per_call, _ = B.time_calls(ctx, [pf], steps, 3)
+        k_s = B.kernel_time(ctx, [pf], steps, 1)
         flops = prefill_flops(n, window)
-        k_s = kms * 1e-3 / max(kn, 1)
         extra[name] = {
             "config": (f"configs[{2 if layer == 0 else 3}]: {'local' if layer == 0 else 'global'} "
                        f"prefill, N={n}, start 0" + (f", window {window}" if window < n else "")),
@@ -378,12 +429,12 @@ def main():
 
     line = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": None if value is None else round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": None if ms_per_step is None else round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -392,17 +443,18 @@ def main():
         "config": {
             "workload": "configs[1]: global-layer decode attention, batch 1, pos 8191, L=8192, "
                         "8 Q / 4 KV heads, head_dim 256, fp32 KV cache",
-            "us_per_token": round(ms_per_step * 1e3, 3),
+            "us_per_token": None if ms_per_step is None else round(ms_per_step * 1e3, 3),
             "bytes_per_step": decode_bytes(8192),
             "llc": "10 distinct 64 MiB caches rotated (640 MiB > 256 MB Infinity Cache)",
         },
-        "roofline": {
+        "roofline": None if achieved is None else {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("decode_kernel<2,true>@configs[1]"),
+            "traffic_source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "kernel": "decode_kernel<2,true>",
             "kernel_us": round(kernel_s * 1e6, 3),
             "call_us": round(call_s * 1e6, 3),

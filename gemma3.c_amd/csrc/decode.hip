@@ -25,6 +25,7 @@
 //   merges them.  A last-arrival combine inside the kernel would need a
 //   device-scope release fence per workgroup, and on gfx950 that writes
 //   back the XCD's whole L2: measured slower than the extra launch.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "g3k.h"
@@ -40,11 +41,11 @@ constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
 // one row so its larger q / acc arrays fit without spills.
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
-constexpr float NEG_BIG = -1.0e30f;
+constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
 // in flight per wave, one contiguous row range per split.  Double-buffered
 // steps, three workgroups per CU and block-cyclic row assignment were each
-// slower or no faster at both 8K and 128K.   // "no row seen yet": finite so exp2 never sees inf - inf
+// slower or no faster at both 8K and 128K.
 
 // x: this lane's 16 dims of one 256-vector (lane c: dims c*4 + 64j + e).
 // RMSNorm with (1 + w) gain (gemma3_kernels.c:289-304), then the NeoX
@@ -407,10 +408,10 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
 template <int G, bool FUSED>
 hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
     dim3 grid(a->n_splits, a->n_kv_heads);
-    if (a->ev0 && hipEventRecord((hipEvent_t)a->ev0, st) != hipSuccess) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((decode_kernel<G, FUSED>), grid, dim3(NT), 0, st, *a);
+    // With timing events the dispatch itself records them (kernel begin / end).
+    hipExtLaunchKernelGGL((decode_kernel<G, FUSED>), grid, dim3(NT), 0, st, (hipEvent_t)a->ev0,
+                          (hipEvent_t)a->ev1, 0, *a);
     hipError_t e = hipGetLastError();
-    if (a->ev1 && hipEventRecord((hipEvent_t)a->ev1, st) != hipSuccess) return hipErrorInvalidValue;
     if (e != hipSuccess || a->n_splits == 1) return e;
     hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 64, G, a->n_kv_heads), dim3(NT), 0, st, *a);
     return hipGetLastError();

@@ -48,7 +48,7 @@ typedef struct {
     float *out;            /* [H_q][D] */
     float *ws_acc;         /* [H_kv][G3K_MAX_SPLITS][group][D] split partials */
     float *ws_ml;          /* [H_kv][G3K_MAX_SPLITS][group][2] (max, sum) */
-    void *ev0, *ev1;       /* hipEvent_t recorded around decode_kernel, or NULL */
+    void *ev0, *ev1;       /* hipEvent_t: begin / end of decode_kernel's dispatch, or NULL */
 } g3k_decode_args;
 
 /* QK-norm + RoPE of q (and of the new k), cache write of the new k/v and
@@ -118,7 +118,7 @@ typedef struct {
     int n, hist, nk, window;  /* window: INT_MAX / 2 for global layers */
     int n_kv_heads, group;
     float qscale;             /* softmax scale * log2(e) */
-    void *ev0, *ev1;          /* hipEvent_t recorded around prefill_kernel, or NULL */
+    void *ev0, *ev1;          /* hipEvent_t: begin / end of prefill_kernel's dispatch, or NULL */
 } g3k_prefill_args;
 
 int g3k_prefill(const g3k_prefill_args *a, void *stream);

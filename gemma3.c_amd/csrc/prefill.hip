@@ -17,34 +17,31 @@
 //             specified on; fp32 accumulation throughout.
 // That is 2.5x the algorithmic MFMA work.
 //
-// Data flow.  One workgroup = 8 wave64 = one KV head x 32*4/G query
-// positions of each of its G query heads.  Waves work in pairs on 32 queries
-// of one head; wave 2p+e owns the head-dim half e (128 dims) of them:
-//   partial S^T[key][query] = K[:, half] . Q[:, half]^T with
-//     v_mfma_f32_32x32x16_f16: A = K tile rows from LDS, B = the wave's Q^T
-//     fragments in registers (hi / lo: 64 VGPRs);
-//   the pair adds its two partial S^T tiles through LDS (4 KiB per wave), both
-//     waves run the same softmax;
-//   O^T[dim in half][query] += V^T . P^T with v_mfma_f32_32x32x16_bf16: A = V^T
-//     tile rows from LDS, B = P straight from the S^T registers (O^T: 64 regs).
-// Splitting the head dim keeps each wave near 200 registers (two waves per
-// SIMD) while every K / V byte staged in LDS still serves 32 queries per MFMA.
-// In the 32x32 accumulator layout lane l holds column (query) l % 32, so the
-// softmax row statistics of a query live in one lane pair (l, l ^ 32) and the
-// O^T rescale is lane-local.  K rows are fed to the MFMA in the order
-// key(m) = m with bits 2 and 3 swapped; then accumulator register r of lane
-// half h holds key 16*(r/8) + 8*h + r%8, which is exactly the B-operand
-// order of the P.V MFMA (no shuffles between the two products).
-// Key tiles of 32 are double-buffered in LDS and fetched one tile ahead with
+// Data flow.  One workgroup = 8 wave64 = one KV head x 16*8/G query
+// positions of each of its G query heads; each wave owns 16 queries of one
+// head over the full head dim (Q^T hi / lo: 64 VGPRs, O^T: 64):
+//   S^T[key][query] = K . Q^T   with v_mfma_f32_16x16x32_f16: A = K tile rows
+//     from LDS, B = the wave's Q^T fragments in registers;
+//   O^T[dim][query] += V^T . P^T with v_mfma_f32_16x16x32_bf16: A = V^T tile
+//     rows from LDS, B = P straight from the S^T registers.
+// In the 16x16 accumulator layout lane l holds column (query) l % 16, so a
+// query's softmax statistics live in the four lanes l % 16 + 16 g and the
+// O^T rescale is lane-local.  The K rows fed to S^T sub-tile j (keys
+// 16 j .. of a 32-key tile) are permuted, row m -> key 8 (m / 4) + 4 j + m % 4,
+// so lane group g = l / 16 ends up holding keys 8 g .. 8 g + 7 in its eight
+// S^T registers: exactly the B operand of the P.V MFMA (no shuffles).
+// Key tiles of 32 are triple-buffered in LDS and fetched two tiles ahead with
 // gfx950's direct global->LDS loads (global_load_lds_dwordx4: no staging
-// registers; each wave instruction fills 1 KiB of LDS in lane order):
-// K_hi, K_lo [32][256] fp16 and V^T [256][32] bf16, unpadded, with the 16-byte
-// chunks of each row XOR-swizzled so that the MFMA fragment reads
-// (ds_read_b128) hit distinct bank groups.  Two barriers per tile (partial-S
-// exchange, stage hand-over).
-// Softmax runs in the exp2 domain (q pre-scaled by scale*log2(e)) with a
-// lazy running max: O and l are rescaled only when a tile's max exceeds the
-// reference max by more than 2^8.
+// registers; one wave instruction moves 1 KiB in lane order):
+//   K: one LDS row per key, fp16 hi (512 B) | lo (512 B), rows padded to
+//      1040 B, so 16 lanes reading 16 rows at one chunk hit 16 bank groups and
+//      every fragment address is a per-lane base + an immediate offset;
+//   V^T: [256][32] bf16, the four 16-byte chunks of a row XOR-swizzled by
+//      row bits 2-3 (conflict-free fragment reads, also base + immediate).
+// One barrier per tile (stage hand-over).  Softmax runs in the exp2 domain
+// (q pre-scaled by scale * log2(e)) with a lazy running max: O and l are
+// rescaled only when a tile's max exceeds the reference max by more than 2^8.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "g3k.h"
@@ -58,16 +55,18 @@ constexpr int D = G3K_HEAD_DIM;
 constexpr int NT = 256;                      // staging kernel
 constexpr int NTA = 512;                     // attention kernel: 8 waves
 constexpr int BK = 32;                       // keys per tile
-constexpr int KTILE = BK * D;                // halves in one K_hi or K_lo tile (16 KiB)
-constexpr int VTILE = D * BK;                // halves in one V^T tile (16 KiB)
-constexpr int STAGE = 2 * KTILE + VTILE;     // halves per pipeline stage (48 KiB)
-constexpr int XCH = 8 * 16 * 64;             // floats of the partial-S exchange (32 KiB)
+constexpr int KROWB = 1040;                  // bytes per K row in LDS: hi | lo | pad
+constexpr int KTILEB = BK * KROWB;           // bytes of the K tile (33280)
+constexpr int VTILEB = D * BK * 2;           // bytes of the V^T tile (16 KiB)
+constexpr int STAGEB = KTILEB + VTILEB;      // bytes per pipeline stage
+constexpr int NSTAGE = 3;                    // tiles in flight: compute kt, fetch kt+1, kt+2
+constexpr int FETCH_OPS = 6;                 // global->LDS instructions per wave per tile
 constexpr float NEG_BIG = -1.0e30f;
 constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint16_t f16_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 
@@ -143,98 +142,83 @@ __global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) {
 // Attention.
 // ---------------------------------------------------------------------------
 
-// Row of the K tile fed to MFMA row m: bits 2 and 3 of m swapped.
-__device__ __forceinline__ int key_of_row(int m) {
-    return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);
-}
-
-// Swizzles of the 16-byte chunks inside an LDS row.  K rows hold 32 chunks
-// (512 B); a fragment read takes chunk 2t + h of rows key_of_row(l % 32):
-// kswz is a bijection on row % 16 with kswz >> 1 distinct over each 8 rows
-// that lanes 0-7 / 8-15 read, so 16 lanes of one chunk, or 8 lanes of each
-// of two adjacent chunks, always fall in 16 different bank groups.  V^T rows
-// hold 4 chunks (64 B); vswz spreads the 4 rows of one bank residue
-// (d, d+4, d+8, d+12) over the 4 chunk positions, in pairs for two chunks.
-__device__ __forceinline__ int kswz(int r) { return 2 * (r & 3) + 8 * ((r >> 3) & 1) + ((r >> 2) & 1); }
-__device__ __forceinline__ int vswz(int d) { return 2 * ((d >> 2) & 1) + ((d >> 3) & 1); }
-
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef const __attribute__((address_space(1))) void *gbl_ptr;
 
-// Direct global -> LDS fetch of key tile kt into stage `st`: 48 one-KiB
-// blocks (16 K_hi, 16 K_lo, 16 V^T), six per wave.
-__device__ __forceinline__ void tile_fetch(uint16_t *st, const g3k_prefill_args &p, int kvh, int kt,
-                                           int wave, int lane) {
-    const uint16_t *kh = p.k_hi + ((size_t)kvh * p.ldk + (size_t)kt * BK) * D;
-    const uint16_t *kl = p.k_lo + ((size_t)kvh * p.ldk + (size_t)kt * BK) * D;
+// XOR swizzle of the four 16-byte chunks of a V^T row: rows d, d+4, d+8,
+// d+12 (one bank residue) take the four chunk positions.
+__device__ __forceinline__ int vswz(int d) { return (d >> 2) & 3; }
+
+// Direct global -> LDS fetch of key tile kt into the stage at byte offset
+// `st`: 32 K rows (lanes 0-31 the hi half, 32-63 the lo half) and 16 V^T
+// blocks of 16 rows; six one-KiB instructions per wave.
+__device__ __forceinline__ void tile_fetch(unsigned char *st, const g3k_prefill_args &p, int kvh,
+                                           int kt, int wave, int lane) {
+    const size_t krow0 = (size_t)kvh * p.ldk + (size_t)kt * BK;
     const uint16_t *vt = p.vt + (size_t)kvh * D * p.ldk + (size_t)kt * BK;
 #pragma unroll
     for (int u = 0; u < 6; u++) {
         const int j = wave * 6 + u;
         if (j < 32) {
-            const int b = j & 15;                   // rows 2b, 2b+1 of a K tile
-            const int r = 2 * b + (lane >> 5);
-            const int c = (lane & 31) ^ kswz(r);
-            const uint16_t *src = (j < 16 ? kh : kl) + (size_t)r * D + c * 8;
-            __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(st + (j >> 4) * KTILE + b * 512),
-                                             16, 0, 0);
+            const uint16_t *src = (lane < 32 ? p.k_hi : p.k_lo) + (krow0 + j) * D + (lane & 31) * 8;
+            __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(st + j * KROWB), 16, 0, 0);
         } else {
             const int b = j - 32;                   // V^T rows 16b .. 16b+15
             const int d = 16 * b + (lane >> 2);
             const int c = (lane & 3) ^ vswz(d);
             __builtin_amdgcn_global_load_lds((gbl_ptr)(vt + (size_t)d * p.ldk + c * 8),
-                                             (lds_ptr)(st + 2 * KTILE + b * 512), 16, 0, 0);
+                                             (lds_ptr)(st + KTILEB + b * 1024), 16, 0, 0);
         }
     }
 }
 
-__device__ __forceinline__ void wait_fetch() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// Workgroup barrier that orders LDS traffic only (ds_write before, ds_read
-// after).  __syncthreads() would also wait for every outstanding global load,
-// including the next tile's global->LDS fetch that is meant to overlap.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+// Wait until this wave's fetches of all but the newest tile have landed
+// (vmcnt counts the global->LDS loads; nothing else is outstanding in the loop).
+__device__ __forceinline__ void wait_fetch_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_fetch_but_one() {
+    static_assert(FETCH_OPS == 6, "vmcnt below assumes six fetch instructions per tile");
+    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
 }
 
 template <int G>
 __global__ __launch_bounds__(NTA, 1) void prefill_kernel(g3k_prefill_args p) {
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
-    __shared__ __attribute__((aligned(16))) float xch[XCH];
-    constexpr int PPG = 4 / G;        // wave pairs per query head
-    constexpr int PB = 32 * PPG;      // query positions per workgroup
+    __shared__ __attribute__((aligned(16))) unsigned char smem[NSTAGE * STAGEB];
+    constexpr int WPH = 8 / G;        // waves per query head
+    constexpr int PB = 16 * WPH;      // query positions per workgroup
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int h = lane >> 5, ln = lane & 31;
-    const int pair = wave >> 1, e = wave & 1;     // e: head-dim half of this wave
-    const int kvh = blockIdx.y;
-    const int qb = gridDim.x - 1 - blockIdx.x;  // longest (latest) query blocks first
-    const int g = pair / PPG;
-    const int qhead = kvh * G + g;
-    const int tok0 = qb * PB + (pair % PPG) * 32;
+    const int g = lane >> 4, ln = lane & 15;     // lane group, query column
+    // 1-D grid, longest (latest) query blocks first across all heads: with
+    // workgroups dealt round-robin to the 8 XCDs, block id -> (qb, id % H_kv)
+    // also keeps each XCD on one KV head (its L2 streams one head's K / V).
+    const int kvh = blockIdx.x % p.n_kv_heads;
+    const int qb = (int)(gridDim.x / p.n_kv_heads) - 1 - (int)(blockIdx.x / p.n_kv_heads);
+    const int qhead = kvh * G + wave / WPH;
+    const int tok0 = qb * PB + (wave % WPH) * 16;
     const int tok = tok0 + ln;
     const bool wave_live = tok0 < p.n;
     const int q_kk = p.hist + tok;    // key index of this lane's query
 
-    // key index range of the workgroup and of this wave pair (inclusive)
+    // key index range of the workgroup and of this wave (inclusive)
     const int wg_first = p.hist + qb * PB;
     const int wg_last = min(p.hist + min(qb * PB + PB, p.n) - 1, p.nk - 1);
     const int kt0 = max(0, wg_first - p.window + 1) / BK;
     const int kt1 = wg_last / BK;
     const int w_first = p.hist + tok0;
-    const int w_last = min(w_first + 31, p.hist + p.n - 1);
+    const int w_last = min(w_first + 15, p.hist + p.n - 1);
     const int wkt0 = max(0, w_first - p.window + 1) / BK;
     const int wkt1 = w_last / BK;
 
-    // ---- first tile in flight, then this wave's Q^T fragments (hi / lo) ----
+    // ---- first two tiles in flight, then this wave's Q^T fragments (hi / lo) ----
     tile_fetch(smem, p, kvh, kt0, wave, lane);
+    if (kt0 + 1 <= kt1) tile_fetch(smem + STAGEB, p, kvh, kt0 + 1, wave, lane);
 
     half8 qh[8], ql[8];
     {
-        const float *qrow = p.q + ((size_t)qhead * p.n + (tok < p.n ? tok : 0)) * D + 128 * e;
+        const float *qrow = p.q + ((size_t)qhead * p.n + (tok < p.n ? tok : 0)) * D + 8 * g;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const float4 a = *reinterpret_cast<const float4 *>(qrow + 16 * t + 8 * h);
-            const float4 b = *reinterpret_cast<const float4 *>(qrow + 16 * t + 8 * h + 4);
+            const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * t);
+            const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * t + 4);
             const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int u = 0; u < 8; u++) {
@@ -246,83 +230,60 @@ __global__ __launch_bounds__(NTA, 1) void prefill_kernel(g3k_prefill_args p) {
         }
     }
 
-    f32x16 o[4];
+    f32x4 o[16];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[mt][r] = 0.f;
+    for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref = NEG_BIG, l_sum = 0.f;
-    const int krow = key_of_row(ln);
-    const int ksw = kswz(krow), vsw = vswz(ln);  // (32*mt + ln) has the same vswz as ln
-    float *x_mine = xch + wave * 1024 + lane * 4;         // [wave][r/4][lane][4]
-    const float *x_other = xch + (wave ^ 1) * 1024 + lane * 4;
+    // per-lane LDS byte offsets inside a stage: K rows of the two S^T
+    // sub-tiles (row m -> key 8 (m / 4) + 4 j + m % 4) at chunk g, and the
+    // V^T row ln of each 16-dim block at its swizzled chunk g
+    const int krow = 8 * (ln >> 2) + (ln & 3);
+    const int koff0 = krow * KROWB + 16 * g;
+    const int koff1 = (krow + 4) * KROWB + 16 * g;
+    const int voff = KTILEB + ln * 64 + 16 * (g ^ vswz(ln));
 
-    wait_fetch();
+    if (kt0 + 1 <= kt1) wait_fetch_but_one(); else wait_fetch_all();
     __syncthreads();
 
+    int cur = 0;                      // stage holding tile kt
     for (int kt = kt0; kt <= kt1; kt++) {
-        const int cur = (kt - kt0) & 1;
-        if (kt < kt1) tile_fetch(smem + (cur ^ 1) * STAGE, p, kvh, kt + 1, wave, lane);
-        const uint16_t *st = smem + cur * STAGE;
-        const bool live = wave_live && kt >= wkt0 && kt <= wkt1;
+        const int nxt2 = cur == 0 ? 2 : cur - 1;    // stage of tile kt + 2 (= kt - 1's)
+        if (kt + 2 <= kt1) tile_fetch(smem + nxt2 * STAGEB, p, kvh, kt + 2, wave, lane);
+        const unsigned char *st = smem + cur * STAGEB;
 
-        // ---- partial S^T over this wave's head-dim half, three fp16 passes ----
-        f32x16 s;
-        if (live) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) s[r] = 0.f;
-            const uint16_t *kh = st + krow * D;
-            const uint16_t *kl = kh + KTILE;
-            // fragments of d-step t + 1 are read while step t's MFMAs run
-            half8 ah = *reinterpret_cast<const half8 *>(kh + ((16 * e + h) ^ ksw) * 8);
-            half8 al = *reinterpret_cast<const half8 *>(kl + ((16 * e + h) ^ ksw) * 8);
+        if (wave_live && kt >= wkt0 && kt <= wkt1) {
+            // ---- S^T = K . Q^T for keys 0-15 (s0) and 16-31 (s1), three fp16 passes ----
+            f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
             for (int t = 0; t < 8; t++) {
-                half8 ah_n = ah, al_n = al;
-                if (t < 7) {
-                    const int cofs = ((16 * e + 2 * t + 2 + h) ^ ksw) * 8;
-                    ah_n = *reinterpret_cast<const half8 *>(kh + cofs);
-                    al_n = *reinterpret_cast<const half8 *>(kl + cofs);
-                }
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[t], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[t], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[t], s, 0, 0, 0);
-                ah = ah_n;
-                al = al_n;
+                const half8 ah0 = *reinterpret_cast<const half8 *>(st + koff0 + 64 * t);
+                const half8 al0 = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * t);
+                const half8 ah1 = *reinterpret_cast<const half8 *>(st + koff1 + 64 * t);
+                const half8 al1 = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * t);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, qh[t], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, qh[t], s1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, ql[t], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, ql[t], s1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al0, qh[t], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al1, qh[t], s1, 0, 0, 0);
             }
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                *reinterpret_cast<float4 *>(x_mine + j * 256) =
-                    make_float4(s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]);
-        }
-        lds_barrier();
-
-        if (live) {
-            // ---- full S^T = half 0 + half 1 (same order in both waves) ----
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float4 y = *reinterpret_cast<const float4 *>(x_other + j * 256);
-                const float yy[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    s[4 * j + i] = e == 0 ? s[4 * j + i] + yy[i] : yy[i] + s[4 * j + i];
-            }
+            // register u of this lane: key kt*32 + 8 g + u (u < 4: s0[u], else s1[u-4])
+            float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
             // ---- mask (diagonal, window edge, ragged end) ----
-            const int kbase = kt * BK + 8 * h;
             const bool edge = (kt * BK + BK - 1 > w_first) || (kt * BK <= w_last - p.window) ||
                               (kt * BK + BK > p.nk);
             if (edge) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int kk = kbase + 16 * (r >> 3) + (r & 7);
+                for (int u = 0; u < 8; u++) {
+                    const int kk = kt * BK + 8 * g + u;
                     const bool ok = kk <= q_kk && kk > q_kk - p.window && kk < p.nk;
-                    s[r] = ok ? s[r] : -INFINITY;
+                    sv[u] = ok ? sv[u] : -INFINITY;
                 }
             }
             // ---- online softmax with a lazy reference max ----
-            float mx = s[0];
-#pragma unroll
-            for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[r]);
+            float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const bool bump = mx > m_ref + LAZY;
             if (__builtin_amdgcn_ballot_w64(bump)) {
@@ -331,65 +292,54 @@ __global__ __launch_bounds__(NTA, 1) void prefill_kernel(g3k_prefill_args p) {
                 m_ref = m_new;
                 l_sum *= alpha;
 #pragma unroll
-                for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) o[mt][r] *= alpha;
+                for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
             }
             float psum = 0.f;
-            bf16x8 ph[2], pl[2];
+            bf16x8 ph, pl;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float pr = s[r] == -INFINITY ? 0.f : fast_exp2(s[r] - m_ref);
+            for (int u = 0; u < 8; u++) {
+                const float pr = fast_exp2(sv[u] - m_ref);   // exp2(-inf) = 0 for masked keys
                 psum += pr;
                 const __bf16 hi = (__bf16)pr;
-                ph[r >> 3][r & 7] = hi;
-                pl[r >> 3][r & 7] = (__bf16)(pr - (float)hi);
+                ph[u] = hi;
+                pl[u] = (__bf16)(pr - (float)hi);
             }
+            psum += __shfl_xor(psum, 16);
             psum += __shfl_xor(psum, 32);
             l_sum += psum;
-            // ---- O^T[half] += V^T . P^T, two bf16 passes ----
-            const uint16_t *vt = st + 2 * KTILE + (128 * e + ln) * BK;
-            bf16x8 av = *reinterpret_cast<const bf16x8 *>(vt + ((h ^ vsw) * 8));
+            // ---- O^T += V^T . P^T, two bf16 passes, 16 dim blocks ----
 #pragma unroll
-            for (int f = 0; f < 8; f++) {          // f = 2 * mt + t2
-                const int mt = f >> 1, t2 = f & 1;
-                bf16x8 av_n = av;
-                if (f < 7) {
-                    const int cofs = ((2 * ((f + 1) & 1) + h) ^ vsw) * 8;
-                    av_n = *reinterpret_cast<const bf16x8 *>(vt + ((f + 1) >> 1) * 32 * BK + cofs);
-                }
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, ph[t2], o[mt], 0, 0, 0);
-                o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pl[t2], o[mt], 0, 0, 0);
-                av = av_n;
+            for (int mt = 0; mt < 16; mt++) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(st + voff + 1024 * mt);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ph, o[mt], 0, 0, 0);
+                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl, o[mt], 0, 0, 0);
             }
         }
 
-        wait_fetch();
+        // tile kt + 1 must have landed before the barrier; kt + 2 may still fly
+        if (kt + 2 <= kt1) wait_fetch_but_one(); else wait_fetch_all();
         __syncthreads();
+        cur = cur == 2 ? 0 : cur + 1;
     }
 
     // ---- normalise and write attn_out[token][qhead][dim] ----
     if (!wave_live || tok >= p.n) return;
     const float inv = 1.0f / l_sum;
-    float *orow = p.out + ((size_t)tok * p.n_kv_heads * G + qhead) * D + 128 * e + 4 * h;
+    float *orow = p.out + ((size_t)tok * p.n_kv_heads * G + qhead) * D + 4 * g;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            *reinterpret_cast<float4 *>(orow + mt * 32 + 8 * j) =
-                make_float4(o[mt][4 * j] * inv, o[mt][4 * j + 1] * inv, o[mt][4 * j + 2] * inv,
-                            o[mt][4 * j + 3] * inv);
+    for (int mt = 0; mt < 16; mt++)
+        *reinterpret_cast<float4 *>(orow + 16 * mt) =
+            make_float4(o[mt][0] * inv, o[mt][1] * inv, o[mt][2] * inv, o[mt][3] * inv);
 }
 
 template <int G>
 hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
-    constexpr int PB = 32 * (4 / G);
+    constexpr int PB = 16 * (8 / G);
     const int nqb = (a->n + PB - 1) / PB;
-    if (a->ev0 && hipEventRecord((hipEvent_t)a->ev0, st) != hipSuccess) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(prefill_kernel<G>, dim3(nqb, a->n_kv_heads), dim3(NTA), 0, st, *a);
-    const hipError_t e = hipGetLastError();
-    if (a->ev1 && hipEventRecord((hipEvent_t)a->ev1, st) != hipSuccess) return hipErrorInvalidValue;
-    return e;
+    // With timing events the dispatch itself records them (kernel begin / end).
+    hipExtLaunchKernelGGL(prefill_kernel<G>, dim3(nqb * a->n_kv_heads), dim3(NTA), 0, st,
+                          (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
+    return hipGetLastError();
 }
 
 }  // namespace

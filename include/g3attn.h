@@ -150,10 +150,11 @@ void *g3attn_stream(g3attn_ctx *ctx);
 int g3attn_synchronize(g3attn_ctx *ctx);
 
 /* Kernel timing for benchmarks (no counterpart in the reference, which has no
- * timers).  While enabled, every decode / prefill call brackets its main
+ * timers).  While enabled, every decode / prefill call times its main
  * attention kernel (kind 0: the split-K decode kernel, without the split
  * combine; kind 1: the prefill MFMA kernel, without the staging kernels)
- * with HIP events on the context stream.  g3attn_profile_read waits for the
+ * with a pair of HIP events that the kernel's own dispatch records (begin
+ * and end of execution) on the context stream.  g3attn_profile_read waits for the
  * stream and returns, for one kind, the launches bracketed since the last
  * read and their summed duration in milliseconds, then resets that kind. */
 int g3attn_profile_enable(g3attn_ctx *ctx, int enable);

@@ -1,0 +1,194 @@
+#!/usr/bin/env python3
+"""Writes the golden fixtures of tests/golden/ from the REAL reference code.
+
+Runs only where oracle/_ref/libg3ref.so was built, i.e. where the reference
+sources (robitec97/gemma3.c: gemma3_kernels.c, gemma3_transformer.c) were
+present at build time; that library is the reference's own code compiled in
+place by oracle/Makefile (never copied).  Inputs come from the oracle's
+seeded generator; each fixture stores the FNV-1a hashes of its inputs so
+generator drift on another machine is caught before outputs are compared.
+
+    python tests/golden/make_golden.py            # all fixtures
+    python tests/golden/make_golden.py --no-big   # skip the configs[3] run (~1-2 min)
+
+Fixtures (numpy .npz, allow_pickle=False):
+  rope.npz        RoPE table bits: full-table hashes + sampled rows
+                  (gemma3_rope_precompute, gemma3_kernels.c:455-468)
+  kernels.npz     rmsnorm / rope_apply / softmax / gqa on seeded vectors
+                  (gemma3_kernels.c:289-304, 470-484, 396-415, 527-597)
+  decode.npz      layer_attention attention section (gemma3_transformer.c:294-352)
+                  at configs[0] (local, pos 511) and configs[1] (global, pos 8191)
+  prefill.npz     the prefill attention loop (gemma3_transformer.c:641-692):
+                  small / chunked / ring-wrap cases, configs[2] and configs[3]:
+                  sampled rows + (sum, sum of squares) of every row, and the
+                  hashes of the final cache
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(REPO, "oracle"))
+import g3_oracle as O  # noqa: E402
+
+QS, KS = 2048, 1024
+
+
+def h64(a) -> np.uint64:
+    return np.uint64(O.fnv1a64(np.ascontiguousarray(a)))
+
+
+def rope_fixture():
+    out = {}
+    for L in (8192, 131072):
+        for theta in (10000.0, 1e6):
+            t = O.rope_table(L, theta, use_ref=True)
+            tag = f"{L}_{int(theta)}"
+            out[f"hash_{tag}"] = h64(t)
+            rows = [p for p in (0, 1, 2, 511, 1023, 4097, 8191, 65536, 131071) if p < L]
+            out[f"rows_{tag}"] = np.array(rows, np.int32)
+            out[f"bits_{tag}"] = t.reshape(L, 256)[rows].view(np.uint32).copy()
+    return out
+
+
+def kernels_fixture():
+    out = {}
+    x = O.gen_normal_bf16(4 * 256, 0x60D1).reshape(4, 256)   # small enough to store
+    w = np.stack([np.zeros(256, np.uint16),
+                  (np.arange(256) * 37 % 200 + 0x3C00).astype(np.uint16)])
+    out["rms_x"], out["rms_w"] = x, w
+    out["rms_y"] = np.stack([O.rmsnorm_bf16(x[i], w[j], use_ref=True) for i in range(4) for j in range(2)])
+    t = O.rope_table(8192, 1e6, use_ref=True)
+    pos = np.array([0, 1, 300, 8191], np.int32)
+    out["rope_pos"] = pos
+    out["rope_y"] = np.stack([O.rope_apply(x[i], t, int(pos[i]), use_ref=True) for i in range(4)])
+    sm = [O.gen_normal_bf16(n, 0x60D2 + n) * 4 for n in (1, 17, 1000)]
+    for i, v in enumerate(sm):
+        out[f"softmax_x{i}"] = v
+        out[f"softmax_y{i}"] = O.softmax(v, use_ref=True)
+    for name, (hq, hkv, L, masked) in {"g1": (8, 4, 1, False), "g2": (8, 4, 17, False),
+                                       "g3": (8, 4, 300, True), "g4": (4, 4, 129, False),
+                                       "g5": (8, 2, 64, True)}.items():
+        q = O.gen_normal_bf16(hq * 256, 0x6100 + L)
+        k = O.gen_normal_bf16(L * hkv * 256, 0x6200 + L)
+        v = O.gen_normal_bf16(L * hkv * 256, 0x6300 + L)
+        mask = None
+        if masked:
+            mask = np.zeros(L, np.float32)
+            mask[::5] = -np.inf
+            mask[1::3] = -1.5
+        # inputs are regenerated from the seeds (0x6100 / 0x6200 / 0x6300 + L)
+        out[f"gqa_{name}_shape"] = np.array([hq, hkv, L, int(masked)], np.int32)
+        out[f"gqa_{name}_in_hash"] = np.array([h64(q), h64(k), h64(v)], np.uint64)
+        out[f"gqa_{name}_y"] = O.gqa(q, k, v, hq, hkv, L, mask=mask, use_ref=True)
+    return out
+
+
+def decode_case(config, layer, pos, max_context):
+    """Inputs of one decode step; the cache holds normed + RoPE'd keys of the
+    earlier positions the layer keeps (reference cache layout)."""
+    cfg = O.Config(max_context=max_context)
+    table = O.rope_table(max_context, cfg.theta(layer), use_ref=True)
+    is_g = O.is_global_layer(layer)
+    lo = 0 if is_g else max(0, pos - cfg.sliding_window)
+    n = pos - lo
+    K = O.gen_normal_bf16(n * KS, O.seed_for(config, 2), lo * KS).reshape(n, KS)
+    V = O.gen_normal_bf16(n * KS, O.seed_for(config, 3), lo * KS).reshape(n, KS)
+    zn = O.zero_norm()
+    O.norm_rope_batch(K.reshape(n, 4, 256), table, lo, zn)
+    rows = cfg.cache_rows(layer)
+    Kc = np.zeros((rows, KS), np.float32)
+    Vc = np.zeros((rows, KS), np.float32)
+    slots = np.arange(lo, pos) if is_g else np.arange(lo, pos) % cfg.sliding_window
+    Kc[slots], Vc[slots] = K, V
+    q = O.gen_normal_bf16(QS, O.seed_for(config, 1))
+    k = O.gen_normal_bf16(KS, O.seed_for(config, 2), pos * KS)
+    v = O.gen_normal_bf16(KS, O.seed_for(config, 3), pos * KS)
+    return cfg, table, q, k, v, Kc, Vc, zn
+
+
+def decode_fixture():
+    out = {}
+    for name, (config, layer, pos, mc) in {"c1": (1, 0, 511, 8192), "c2": (2, 5, 8191, 8192),
+                                           "ring": (8, 0, 1500, 8192)}.items():
+        cfg, table, q, k, v, Kc, Vc, zn = decode_case(config, layer, pos, mc)
+        out[f"{name}_in_hash"] = np.array([h64(q), h64(k), h64(v), h64(Kc), h64(Vc)], np.uint64)
+        out[f"{name}_meta"] = np.array([config, layer, pos, mc], np.int32)
+        o, q_rot, k_rot = O.ref_layer_decode(cfg, layer, pos, q, k, v, Kc, Vc, table, zn, zn)
+        out[f"{name}_out"], out[f"{name}_q_rot"], out[f"{name}_k_rot"] = o, q_rot, k_rot
+    return out
+
+
+def prefill_inputs(config, start, n, layer, max_context=8192):
+    cfg = O.Config(max_context=max_context)
+    table = O.rope_table(max_context, cfg.theta(layer), use_ref=True)
+    s = lambda t: O.seed_for(config, t)
+    Q = O.gen_normal_bf16(n * QS, s(1), start * QS).reshape(n, QS)
+    K = O.gen_normal_bf16(n * KS, s(2), start * KS).reshape(n, KS)
+    V = O.gen_normal_bf16(n * KS, s(3), start * KS).reshape(n, KS)
+    rows = cfg.cache_rows(layer)
+    Kc = np.zeros((rows, KS), np.float32)
+    Vc = np.zeros((rows, KS), np.float32)
+    is_g = O.is_global_layer(layer)
+    lo = 0 if is_g else max(0, start - cfg.sliding_window)
+    if start > lo:
+        hK = O.gen_normal_bf16((start - lo) * KS, s(2), lo * KS).reshape(-1, KS)
+        hV = O.gen_normal_bf16((start - lo) * KS, s(3), lo * KS).reshape(-1, KS)
+        O.norm_rope_batch(hK.reshape(-1, 4, 256), table, lo, O.zero_norm())
+        p = np.arange(lo, start)
+        sl = p if is_g else p % cfg.sliding_window
+        Kc[sl], Vc[sl] = hK, hV
+    return cfg, table, Q, K, V, Kc, Vc
+
+
+def row_sums(out):
+    o = out.astype(np.float64)
+    return np.stack([o.sum(1), (o * o).sum(1)], 1)
+
+
+def prefill_fixture(big: bool):
+    out = {}
+    cases = {"small_g": (40, 0, 64, 5), "chunk_g": (41, 100, 50, 11),
+             "chunk_l": (42, 1000, 80, 0), "wrap_l": (43, 1500, 40, 3),
+             "c3": (3, 0, 2048, 0)}
+    if big:
+        cases["c4"] = (4, 0, 8192, 5)
+    for name, (config, start, n, layer) in cases.items():
+        t0 = time.time()
+        cfg, table, Q, K, V, Kc, Vc = prefill_inputs(config, start, n, layer)
+        out[f"{name}_meta"] = np.array([config, start, n, layer], np.int32)
+        out[f"{name}_in_hash"] = np.array([h64(Q), h64(K), h64(V), h64(Kc), h64(Vc)], np.uint64)
+        zn = O.zero_norm()
+        o, _, _ = O.ref_prefill(cfg, layer, start, Q, K, V, Kc, Vc, table, zn, zn)
+        rows = np.unique(np.concatenate([np.arange(0, min(n, 3)),
+                                         np.linspace(0, n - 1, 6).astype(int)]))
+        out[f"{name}_rows"] = rows.astype(np.int32)
+        out[f"{name}_out_rows"] = o[rows]
+        out[f"{name}_row_sums"] = row_sums(o)
+        out[f"{name}_cache_hash"] = np.array([h64(Kc), h64(Vc)], np.uint64)
+        print(f"  prefill {name}: {time.time() - t0:.1f} s", flush=True)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--no-big", action="store_true")
+    args = ap.parse_args()
+    if not O.have_ref():
+        sys.exit("oracle/_ref/libg3ref.so is not built (needs /root/reference at build time)")
+    for name, fn in (("rope", rope_fixture), ("kernels", kernels_fixture), ("decode", decode_fixture),
+                     ("prefill", lambda: prefill_fixture(not args.no_big))):
+        t0 = time.time()
+        data = fn()
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **data)
+        print(f"{name}.npz: {len(data)} arrays, {time.time() - t0:.1f} s", flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -76,9 +76,9 @@ typedef struct {
     int ring;              /* >0: slot = pos % ring; 0: slot = pos - dst_pos0 */
     int dst_pos0;
     int kv_skip;           /* tokens i < kv_skip are not written to k_dst / v_dst */
-    /* optional prefill staging of the rotated keys, fp16 hi / lo parts
-     * (bit patterns), [n_kv_heads][ldk][D], token i at row row0 + i */
-    uint16_t *k_hi, *k_lo;
+    /* optional prefill staging of the rotated keys, fp16 hi | lo rows
+     * (bit patterns), kq [n_kv_heads][ldk][2][D], token i at row row0 + i */
+    uint16_t *kq;
     long long ldk;
     int row0;
 } g3k_rope_write_args;
@@ -86,8 +86,10 @@ typedef struct {
 int g3k_rope_write(const g3k_rope_write_args *a, void *stream);
 
 /* Prefill staging of key rows kk0..kk0+cnt-1 (key index kk = position -
- * kstart): K (already normed + rotated, fp32) -> fp16 hi / lo rows of
- * k_hi / k_lo [H_kv][ldk][D]; V (fp32) -> bf16 columns of vt [H_kv][D][ldk].
+ * kstart): K (already normed + rotated, fp32) -> fp16 hi | lo rows of
+ * kq [H_kv][ldk][2][D]; V (fp32) -> bf16 hi and lo columns of vt / vt_lo
+ * [H_kv][D][ldk] (v = hi + lo to 16 bits).  If any staged V has a nonzero lo
+ * part, *v_lo_flag is set to epoch.
  * Source row of key kk (position pos = kstart + kk) for head h:
  *   src + h*head_stride + r*row_stride, r = ring ? pos % ring : pos - row_pos0.
  * k_src == NULL stages V only.  Key indices in [nk, kk0+cnt) are written as
@@ -97,27 +99,39 @@ typedef struct {
     long long head_stride, row_stride;
     int ring, row_pos0, kstart;
     int kk0, cnt, nk, n_kv_heads;
-    uint16_t *k_hi, *k_lo, *vt;
+    uint16_t *kq, *vt, *vt_lo;
     long long ldk;
+    int *v_lo_flag;
+    int epoch;
 } g3k_stage_args;
 
 int g3k_stage(const g3k_stage_args *a, void *stream);
 
 /* Causal / sliding-window prefill attention on MFMA (one launch).
- *   q:  normed + rotated queries, fp32 head-major [H_q][n][D]; token i has
- *       key index hist + i.
- *   k_hi / k_lo: fp16 split keys [H_kv][ldk][D]; vt: bf16 values [H_kv][D][ldk],
- *       nk valid key indices, zero padded to ldk (a multiple of 64).
+ *   q:  raw (pre-norm) queries [n][n_heads][D] fp32, the reference's Q_all
+ *       layout; the kernel applies QK-norm (q_norm, NULL = none) and RoPE
+ *       (table row start_pos + i) to token i, whose key index is hist + i.
+ *   kq: fp16 split keys [H_kv][ldk][2][D] (hi | lo rows); vt / vt_lo: bf16
+ *       hi / lo values [H_kv][D][ldk], nk valid key indices, zero padded to
+ *       ldk (a multiple of 64).  vt_lo is read only when *v_lo_flag == epoch
+ *       (some staged V is not exactly bf16).
  *   Query i attends key indices kk with hist+i-window < kk <= hist+i.
  *   out: [n][H_q][D] fp32 (the reference's attn_out layout). */
 typedef struct {
     const float *q;
-    const uint16_t *k_hi, *k_lo, *vt;
+    const uint16_t *q_norm;
+    const float *rope;        /* full table [max_context][D/2][2] */
+    float eps;
+    int start_pos;
+    const uint16_t *kq, *vt, *vt_lo;
+    const int *v_lo_flag;
+    int epoch;
     float *out;
     long long ldk;
     int n, hist, nk, window;  /* window: INT_MAX / 2 for global layers */
     int n_kv_heads, group;
     float qscale;             /* softmax scale * log2(e) */
+    int queries_per_wave;     /* 16 (8 waves, 2 per SIMD) or 32 (4 waves, 1 per SIMD) */
     void *ev0, *ev1;          /* hipEvent_t: begin / end of prefill_kernel's dispatch, or NULL */
 } g3k_prefill_args;
 

@@ -6,20 +6,22 @@
 // or [0, pos] (global layer), pos = start_pos + i, with the reference's
 // softmax (gemma3_kernels.c:396-415) and scale 1/sqrt(head_dim).
 //
-// Precision policy.  Post-RoPE q and k are fp32 and not representable in
-// any MFMA input format, and the path is held to max-abs error <= 2e-3 x
-// output RMS.  A single bf16 or fp16 pass misses that bar by 5-60x on the
-// early causal rows, so:
-//   S = q.k   as three fp16 MFMA passes  q_hi.k_hi + q_lo.k_hi + q_hi.k_lo,
-//             x_hi = fp16(x), x_lo = fp16(x - x_hi)  (about 22 bits);
-//   O = P.V   as two bf16 MFMA passes    P_hi.V + P_lo.V  (16 bits of P),
-//             V in bf16, exact for the bf16-valued inputs the path is
-//             specified on; fp32 accumulation throughout.
-// That is 2.5x the algorithmic MFMA work.
+// Precision policy.  Post-RoPE q and k, P and V are fp32 and not
+// representable in any MFMA input format, and the path is held to max-abs
+// error <= 2e-3 x output RMS.  A single bf16 or fp16 pass misses that bar by
+// 5-60x on the early causal rows, so every operand is split, x = x_hi + x_lo:
+//   S = q.k   three fp16 MFMA passes  q_hi.k_hi + q_lo.k_hi + q_hi.k_lo
+//             (x_hi = fp16(x), x_lo = fp16(x - x_hi): about 22 bits);
+//   O = P.V   bf16 MFMA passes        P_hi.V_hi + P_lo.V_hi (+ P_hi.V_lo)
+//             (16 bits of P and V).  The staging pass records whether any
+//             V_lo is nonzero; when every staged value is exactly bf16 (the
+//             bf16-valued inputs the path is specified on) V_lo is zero and
+//             its pass is skipped, which changes no bit of the result.
+// fp32 accumulation throughout: 2.5x (3x with V_lo) the algorithmic MFMA work.
 //
-// Data flow.  One workgroup = 8 wave64 = one KV head x 16*8/G query
-// positions of each of its G query heads; each wave owns 16 queries of one
-// head over the full head dim (Q^T hi / lo: 64 VGPRs, O^T: 64):
+// Data flow.  One workgroup = 8 / NQB waves = one KV head x the queries of
+// its G query heads; each wave owns NQB blocks of 16 queries of one head over
+// the full head dim (per block Q^T hi / lo: 64 VGPRs, O^T: 64):
 //   S^T[key][query] = K . Q^T   with v_mfma_f32_16x16x32_f16: A = K tile rows
 //     from LDS, B = the wave's Q^T fragments in registers;
 //   O^T[dim][query] += V^T . P^T with v_mfma_f32_16x16x32_bf16: A = V^T tile
@@ -30,17 +32,21 @@
 // 16 j .. of a 32-key tile) are permuted, row m -> key 8 (m / 4) + 4 j + m % 4,
 // so lane group g = l / 16 ends up holding keys 8 g .. 8 g + 7 in its eight
 // S^T registers: exactly the B operand of the P.V MFMA (no shuffles).
-// Key tiles of 32 are triple-buffered in LDS and fetched two tiles ahead with
-// gfx950's direct global->LDS loads (global_load_lds_dwordx4: no staging
-// registers; one wave instruction moves 1 KiB in lane order):
+// Key tiles of 32 live in two LDS rings, K tiles two deep and V^T tiles two
+// deep, filled by gfx950's direct buffer -> LDS loads (buffer_load_dwordx4
+// ... lds: no staging registers; one wave instruction moves 1 KiB in lane
+// order; the addresses are a scalar buffer descriptor + one per-lane offset):
 //   K: one LDS row per key, fp16 hi (512 B) | lo (512 B), rows padded to
-//      1040 B, so 16 lanes reading 16 rows at one chunk hit 16 bank groups and
-//      every fragment address is a per-lane base + an immediate offset;
-//   V^T: [256][32] bf16, the four 16-byte chunks of a row XOR-swizzled by
-//      row bits 2-3 (conflict-free fragment reads, also base + immediate).
-// One barrier per tile (stage hand-over).  Softmax runs in the exp2 domain
-// (q pre-scaled by scale * log2(e)) with a lazy running max: O and l are
-// rescaled only when a tile's max exceeds the reference max by more than 2^8.
+//      1040 B and placed at slot kslot(key), so the 16 rows one fragment read
+//      touches hit 16 bank groups, and every fragment address is a per-lane
+//      base + an immediate offset;
+//   V^T: [256][32] bf16 (then the lo part), the four 16-byte chunks of a row
+//      XOR-swizzled by row bits 2-3 (conflict-free fragment reads).
+// Iteration kt computes the scores of tile kt + 1 and the P.V of tile kt,
+// while K of tile kt + 2 and V of tile kt + 1 stream in; one barrier per
+// tile.  Softmax runs in the exp2 domain (q pre-scaled by scale * log2(e))
+// with a lazy running max: O and l are rescaled only when a tile's max
+// exceeds the reference max by more than 2^8.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -53,14 +59,12 @@ using namespace g3k;
 
 constexpr int D = G3K_HEAD_DIM;
 constexpr int NT = 256;                      // staging kernel
-constexpr int NTA = 512;                     // attention kernel: 8 waves
 constexpr int BK = 32;                       // keys per tile
 constexpr int KROWB = 1040;                  // bytes per K row in LDS: hi | lo | pad
-constexpr int KTILEB = BK * KROWB;           // bytes of the K tile (33280)
-constexpr int VTILEB = D * BK * 2;           // bytes of the V^T tile (16 KiB)
-constexpr int STAGEB = KTILEB + VTILEB;      // bytes per pipeline stage
-constexpr int NSTAGE = 3;                    // tiles in flight: compute kt, fetch kt+1, kt+2
-constexpr int FETCH_OPS = 6;                 // global->LDS instructions per wave per tile
+constexpr int KTILEB = BK * KROWB;           // bytes of a K tile (33280)
+constexpr int VTILEB = D * BK * 2;           // bytes of a V^T tile, one part (16 KiB)
+constexpr int LDS_V0 = 2 * KTILEB;           // V ring after the K ring
+constexpr int LDS_BYTES = LDS_V0 + 2 * 2 * VTILEB;   // 132096
 constexpr float NEG_BIG = -1.0e30f;
 constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 
@@ -69,17 +73,20 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint16_t f16_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+__device__ __forceinline__ uint16_t bf16_bits(__bf16 h) { return __builtin_bit_cast(uint16_t, h); }
 
 // ---------------------------------------------------------------------------
-// Staging: fp32 K rows -> fp16 hi / lo rows, fp32 V rows -> bf16 V^T columns.
-// Workgroup = 64 keys x 64 dims of one head (grid: key blocks, D/64, H_kv).
+// Staging: fp32 K rows -> fp16 hi | lo rows, fp32 V rows -> bf16 hi and lo
+// V^T columns.  Workgroup = 64 keys x 64 dims of one head (grid: key blocks,
+// D/64, H_kv).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) {
-    __shared__ uint16_t s_t[64][64 + 8];
+    __shared__ uint16_t s_t[2][64][64 + 8];
     const int kb = blockIdx.x, dx = blockIdx.y, h = blockIdx.z;
     const int tid = threadIdx.x;
     const int kkbase = a.kk0 + kb * 64;
     const int kend = a.kk0 + a.cnt;
+    int any_lo = 0;
     // four float4 per thread: key row r = c / 16, float4 column c % 16
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -104,32 +111,39 @@ __global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) {
                 hi[e] = f16_bits(xh);
                 lo[e] = f16_bits((_Float16)(x[e] - (float)xh));
             }
-            const size_t o = ((size_t)h * a.ldk + kk) * D + dx * 64 + col;
-            *reinterpret_cast<uint2 *>(a.k_hi + o) =
+            uint16_t *row = a.kq + ((size_t)h * a.ldk + kk) * (2 * D) + dx * 64 + col;
+            *reinterpret_cast<uint2 *>(row) =
                 make_uint2(hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16);
-            *reinterpret_cast<uint2 *>(a.k_lo + o) =
+            *reinterpret_cast<uint2 *>(row + D) =
                 make_uint2(lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16);
         }
-        s_t[col + 0][r] = __builtin_bit_cast(uint16_t, (__bf16)vv.x);
-        s_t[col + 1][r] = __builtin_bit_cast(uint16_t, (__bf16)vv.y);
-        s_t[col + 2][r] = __builtin_bit_cast(uint16_t, (__bf16)vv.z);
-        s_t[col + 3][r] = __builtin_bit_cast(uint16_t, (__bf16)vv.w);
-    }
-    __syncthreads();
-    // V^T: dim row d (64 of them) x 64 keys = 128 B; 8 threads per row, 16 B each
+        const float y[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+        for (int e = 0; e < 4; e++) {
+            const __bf16 yh = (__bf16)y[e];
+            const uint16_t lo = bf16_bits((__bf16)(y[e] - (float)yh));
+            s_t[0][col + e][r] = bf16_bits(yh);
+            s_t[1][col + e][r] = lo;
+            any_lo |= lo & 0x7fff;
+        }
+    }
+    if (__syncthreads_or(any_lo) && tid == 0) *a.v_lo_flag = a.epoch;
+    // V^T: dim row d (64 of them) x 64 keys = 128 B per part; 8 threads per
+    // row, 16 B each
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
         const int c = tid + NT * u;
-        const int d = c >> 3, part = c & 7;
-        const int kk = kkbase + part * 8;
+        const int part = c >> 9;                 // 0: hi, 1: lo
+        const int d = (c >> 3) & 63, seg = c & 7;
+        const int kk = kkbase + seg * 8;
         if (kk >= kend) continue;
-        const uint16_t *s = &s_t[d][part * 8];
+        const uint16_t *s = &s_t[part][d][seg * 8];
         uint4 w;
         w.x = s[0] | (uint32_t)s[1] << 16;
         w.y = s[2] | (uint32_t)s[3] << 16;
         w.z = s[4] | (uint32_t)s[5] << 16;
         w.w = s[6] | (uint32_t)s[7] << 16;
-        uint16_t *dst = a.vt + ((size_t)h * D + dx * 64 + d) * a.ldk + kk;
+        uint16_t *dst = (part ? a.vt_lo : a.vt) + ((size_t)h * D + dx * 64 + d) * a.ldk + kk;
         if (kk + 8 <= kend) {
             *reinterpret_cast<uint4 *>(dst) = w;
         } else {
@@ -143,48 +157,168 @@ __global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) {
 // ---------------------------------------------------------------------------
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
-typedef const __attribute__((address_space(1))) void *gbl_ptr;
 
 // XOR swizzle of the four 16-byte chunks of a V^T row: rows d, d+4, d+8,
 // d+12 (one bank residue) take the four chunk positions.
 __device__ __forceinline__ int vswz(int d) { return (d >> 2) & 3; }
 
-// Direct global -> LDS fetch of key tile kt into the stage at byte offset
-// `st`: 32 K rows (lanes 0-31 the hi half, 32-63 the lo half) and 16 V^T
-// blocks of 16 rows; six one-KiB instructions per wave.
-__device__ __forceinline__ void tile_fetch(unsigned char *st, const g3k_prefill_args &p, int kvh,
-                                           int kt, int wave, int lane) {
-    const size_t krow0 = (size_t)kvh * p.ldk + (size_t)kt * BK;
-    const uint16_t *vt = p.vt + (size_t)kvh * D * p.ldk + (size_t)kt * BK;
+// LDS slot of key row r of a tile.  A K fragment read touches the rows
+// {0-3, 8-11, 16-19, 24-27} (or that set + 4) at one chunk; with 1040-byte
+// rows the bank group is slot % 16, so rows r and r + 16 would collide.
+// Flipping bit 2 of the upper half's rows makes each read set hit all 16
+// bank groups.
+__device__ __forceinline__ int kslot(int r) { return r ^ ((r >> 4) << 2); }
+
+// Raw buffer descriptor over [base, base + bytes): stride 0, the gfx9
+// family's dword-3 format word for untyped access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// K tile kt -> LDS ring slot `dst`: 32 rows of 1 KiB (hi | lo), lane l moves
+// bytes 16 l .. 16 l + 15 of the row; 32 / NW rows per wave.
+template <int NW>
+__device__ __forceinline__ void fetch_k(unsigned char *dst, __amdgpu_buffer_rsrc_t kr, int kt, int wave,
+                                        int lane) {
 #pragma unroll
-    for (int u = 0; u < 6; u++) {
-        const int j = wave * 6 + u;
-        if (j < 32) {
-            const uint16_t *src = (lane < 32 ? p.k_hi : p.k_lo) + (krow0 + j) * D + (lane & 31) * 8;
-            __builtin_amdgcn_global_load_lds((gbl_ptr)src, (lds_ptr)(st + j * KROWB), 16, 0, 0);
-        } else {
-            const int b = j - 32;                   // V^T rows 16b .. 16b+15
-            const int d = 16 * b + (lane >> 2);
-            const int c = (lane & 3) ^ vswz(d);
-            __builtin_amdgcn_global_load_lds((gbl_ptr)(vt + (size_t)d * p.ldk + c * 8),
-                                             (lds_ptr)(st + KTILEB + b * 1024), 16, 0, 0);
-        }
+    for (int u = 0; u < 32 / NW; u++) {
+        const int j = wave * (32 / NW) + u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(dst + kslot(j) * KROWB), 16, lane * 16,
+                                                 (kt * BK + j) * (4 * D), 0, 0);
     }
 }
 
-// Wait until this wave's fetches of all but the newest tile have landed
-// (vmcnt counts the global->LDS loads; nothing else is outstanding in the loop).
-__device__ __forceinline__ void wait_fetch_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-__device__ __forceinline__ void wait_fetch_but_one() {
-    static_assert(FETCH_OPS == 6, "vmcnt below assumes six fetch instructions per tile");
-    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+// One part (hi or lo) of V^T tile kt -> LDS: 16 blocks of 16 rows x 64 B;
+// lane l moves row 16 b + l / 4, chunk (l % 4) ^ vswz(row) (voff), so LDS
+// position c of a row holds global chunk c ^ vswz(row).  16 / NW blocks per
+// wave.
+template <int NW>
+__device__ __forceinline__ void fetch_v(unsigned char *dst, __amdgpu_buffer_rsrc_t vr, int kt, int wave,
+                                        unsigned voff, int ldk) {
+#pragma unroll
+    for (int u = 0; u < 16 / NW; u++) {
+        const int b = wave * (16 / NW) + u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_ptr)(dst + b * 1024), 16, voff,
+                                                 (16 * b * ldk + kt * BK) * 2, 0, 0);
+    }
 }
 
-template <int G>
-__global__ __launch_bounds__(NTA, 1) void prefill_kernel(g3k_prefill_args p) {
-    __shared__ __attribute__((aligned(16))) unsigned char smem[NSTAGE * STAGEB];
-    constexpr int WPH = 8 / G;        // waves per query head
-    constexpr int PB = 16 * WPH;      // query positions per workgroup
+// Wait until this wave's buffer->LDS fetches have landed (vmcnt counts them;
+// nothing else is outstanding in the loop).
+__device__ __forceinline__ void wait_fetch_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Keeps the compiler's scheduler from moving instructions across this point:
+// used to hold fragment reads one step ahead of the MFMAs that consume them.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// S^T of one key tile for this wave's NQB blocks of 16 queries: keys 0-15
+// (s[b][0]) and 16-31 (s[b][1]) of the tile, three fp16 passes (k_hi q_hi,
+// k_hi q_lo, k_lo q_hi).  Every K fragment read from LDS feeds all NQB query
+// blocks; the fragments of d-step t + 1 are read while step t's MFMAs run.
+template <int NQB>
+__device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned char *st, int koff0,
+                                            int koff1, const half8 (&qh)[NQB][8],
+                                            const half8 (&ql)[NQB][8]) {
+#pragma unroll
+    for (int b = 0; b < NQB; b++) s[b][0] = s[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    half8 f[2][4];
+    f[0][0] = *reinterpret_cast<const half8 *>(st + koff0);
+    f[0][1] = *reinterpret_cast<const half8 *>(st + koff0 + 512);
+    f[0][2] = *reinterpret_cast<const half8 *>(st + koff1);
+    f[0][3] = *reinterpret_cast<const half8 *>(st + koff1 + 512);
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const int c = t & 1, n = c ^ 1;
+        if (t < 7) {
+            f[n][0] = *reinterpret_cast<const half8 *>(st + koff0 + 64 * (t + 1));
+            f[n][1] = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * (t + 1));
+            f[n][2] = *reinterpret_cast<const half8 *>(st + koff1 + 64 * (t + 1));
+            f[n][3] = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * (t + 1));
+        }
+        sched_fence();
+#pragma unroll
+        for (int b = 0; b < NQB; b++) {
+            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], qh[b][t], s[b][0], 0, 0, 0);
+            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], qh[b][t], s[b][1], 0, 0, 0);
+            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], ql[b][t], s[b][0], 0, 0, 0);
+            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], ql[b][t], s[b][1], 0, 0, 0);
+            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][1], qh[b][t], s[b][0], 0, 0, 0);
+            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][3], qh[b][t], s[b][1], 0, 0, 0);
+        }
+        sched_fence();
+    }
+}
+
+// Loads, QK-norms and rotates (gemma3_kernels.c:289-304, 470-484) one block of
+// 16 queries into the B-operand layout and splits it into fp16 hi / lo.
+// Lane (ln, g) holds dims 32 t + 8 g + u; dim d < 128 and its RoPE partner
+// d + 128 are t and t + 4 of the same lane.
+__device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], const g3k_prefill_args &p,
+                                             int tok, int qhead, int n_heads, int g) {
+    const bool qv = tok < p.n;
+    const float *qrow = p.q + ((size_t)(qv ? tok : 0) * n_heads + qhead) * D + 8 * g;
+    float x[8][8];
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * t);
+        const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * t + 4);
+        x[t][0] = a.x; x[t][1] = a.y; x[t][2] = a.z; x[t][3] = a.w;
+        x[t][4] = b.x; x[t][5] = b.y; x[t][6] = b.z; x[t][7] = b.w;
+    }
+    if (p.q_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int u = 0; u < 8; u++) ss += x[t][u] * x[t][u];
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        const float r = 1.0f / sqrtf(ss / (float)D + p.eps);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint4 wv = *reinterpret_cast<const uint4 *>(p.q_norm + 32 * t + 8 * g);
+            const uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                x[t][u] = x[t][u] * r * (1.0f + bf16f((w[u >> 1] >> (16 * (u & 1))) & 0xffff));
+        }
+    }
+    const float *rrow = p.rope + (size_t)(p.start_pos + (qv ? tok : 0)) * D + 2 * 8 * g;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const float4 cs = *reinterpret_cast<const float4 *>(rrow + 64 * t + 4 * h);
+            const float c[2] = {cs.x, cs.z}, sn[2] = {cs.y, cs.w};
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int u = 2 * h + e;
+                const float a = x[t][u], b = x[t + 4][u];
+                x[t][u] = a * c[e] - b * sn[e];
+                x[t + 4][u] = a * sn[e] + b * c[e];
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float v = qv ? x[t][u] * p.qscale : 0.f;
+            const _Float16 hi = (_Float16)v;
+            qh[t][u] = hi;
+            ql[t][u] = (_Float16)(v - (float)hi);
+        }
+}
+
+// One workgroup's attention: 8 / NQB waves, each owning NQB blocks of 16
+// queries of one head over the full head dim.  VLO adds the P_hi.V_lo pass.
+template <int G, int NQB, bool VLO>
+__device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char *smem) {
+    constexpr int NW = 8 / NQB;       // waves per workgroup
+    constexpr int WPH = NW / G;       // waves per query head
+    constexpr int QW = 16 * NQB;      // queries per wave
+    constexpr int PB = QW * WPH;      // query positions per workgroup
+    constexpr int VST = VTILEB * (VLO ? 2 : 1);   // V ring slot: hi (| lo)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, ln = lane & 15;     // lane group, query column
     // 1-D grid, longest (latest) query blocks first across all heads: with
@@ -193,10 +327,8 @@ __global__ __launch_bounds__(NTA, 1) void prefill_kernel(g3k_prefill_args p) {
     const int kvh = blockIdx.x % p.n_kv_heads;
     const int qb = (int)(gridDim.x / p.n_kv_heads) - 1 - (int)(blockIdx.x / p.n_kv_heads);
     const int qhead = kvh * G + wave / WPH;
-    const int tok0 = qb * PB + (wave % WPH) * 16;
-    const int tok = tok0 + ln;
+    const int tok0 = qb * PB + (wave % WPH) * QW;
     const bool wave_live = tok0 < p.n;
-    const int q_kk = p.hist + tok;    // key index of this lane's query
 
     // key index range of the workgroup and of this wave (inclusive)
     const int wg_first = p.hist + qb * PB;
@@ -204,140 +336,191 @@ __global__ __launch_bounds__(NTA, 1) void prefill_kernel(g3k_prefill_args p) {
     const int kt0 = max(0, wg_first - p.window + 1) / BK;
     const int kt1 = wg_last / BK;
     const int w_first = p.hist + tok0;
-    const int w_last = min(w_first + 15, p.hist + p.n - 1);
+    const int w_last = min(w_first + QW - 1, p.hist + p.n - 1);
     const int wkt0 = max(0, w_first - p.window + 1) / BK;
     const int wkt1 = w_last / BK;
 
-    // ---- first two tiles in flight, then this wave's Q^T fragments (hi / lo) ----
-    tile_fetch(smem, p, kvh, kt0, wave, lane);
-    if (kt0 + 1 <= kt1) tile_fetch(smem + STAGEB, p, kvh, kt0 + 1, wave, lane);
+    // this KV head's staged keys and values as buffer descriptors
+    const int ldk = (int)p.ldk;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(p.kq + (size_t)kvh * ldk * (2 * D), (unsigned)ldk * (4 * D));
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(p.vt + (size_t)kvh * D * ldk, (unsigned)ldk * (2 * D));
+    const __amdgpu_buffer_rsrc_t vlr = make_rsrc(p.vt_lo + (size_t)kvh * D * ldk, (unsigned)ldk * (2 * D));
+    const unsigned voff_v = (unsigned)((lane >> 2) * ldk * 2 + ((lane & 3) ^ ((lane >> 4) & 3)) * 16);
+    auto kbuf = [&](int kt) { return smem + (kt & 1) * KTILEB; };
+    auto vbuf = [&](int kt) { return smem + LDS_V0 + (kt & 1) * VST; };
+    auto fetch_vt = [&](int kt) {
+        fetch_v<NW>(vbuf(kt), vr, kt, wave, voff_v, ldk);
+        if (VLO) fetch_v<NW>(vbuf(kt) + VTILEB, vlr, kt, wave, voff_v, ldk);
+    };
 
-    half8 qh[8], ql[8];
-    {
-        const float *qrow = p.q + ((size_t)qhead * p.n + (tok < p.n ? tok : 0)) * D + 8 * g;
+    // ---- K of the first two tiles and V of the first in flight, then this
+    // wave's queries ----
+    fetch_k<NW>(kbuf(kt0), kr, kt0, wave, lane);
+    if (kt0 + 1 <= kt1) fetch_k<NW>(kbuf(kt0 + 1), kr, kt0 + 1, wave, lane);
+    fetch_vt(kt0);
+
+    half8 qh[NQB][8], ql[NQB][8];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * t);
-            const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * t + 4);
-            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    for (int b = 0; b < NQB; b++)
+        load_queries(qh[b], ql[b], p, tok0 + 16 * b + ln, qhead, p.n_kv_heads * G, g);
+
+    f32x4 o[NQB][16];
+    float m_ref[NQB], l_sum[NQB];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const float v = tok < p.n ? x[u] * p.qscale : 0.f;
-                const _Float16 hi = (_Float16)v;
-                qh[t][u] = hi;
-                ql[t][u] = (_Float16)(v - (float)hi);
-            }
-        }
+    for (int b = 0; b < NQB; b++) {
+        m_ref[b] = NEG_BIG;
+        l_sum[b] = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 16; mt++) o[b][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-
-    f32x4 o[16];
-#pragma unroll
-    for (int mt = 0; mt < 16; mt++) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_ref = NEG_BIG, l_sum = 0.f;
-    // per-lane LDS byte offsets inside a stage: K rows of the two S^T
-    // sub-tiles (row m -> key 8 (m / 4) + 4 j + m % 4) at chunk g, and the
-    // V^T row ln of each 16-dim block at its swizzled chunk g
+    // per-lane LDS byte offsets: K rows of the two S^T sub-tiles (row m ->
+    // key 8 (m / 4) + 4 j + m % 4) at chunk g, and the V^T row ln of each
+    // 16-dim block at its swizzled chunk g
     const int krow = 8 * (ln >> 2) + (ln & 3);
-    const int koff0 = krow * KROWB + 16 * g;
-    const int koff1 = (krow + 4) * KROWB + 16 * g;
-    const int voff = KTILEB + ln * 64 + 16 * (g ^ vswz(ln));
+    const int koff0 = kslot(krow) * KROWB + 16 * g;
+    const int koff1 = kslot(krow + 4) * KROWB + 16 * g;
+    const int voff = ln * 64 + 16 * (g ^ vswz(ln));
 
-    if (kt0 + 1 <= kt1) wait_fetch_but_one(); else wait_fetch_all();
+    wait_fetch_all();
     __syncthreads();
 
-    int cur = 0;                      // stage holding tile kt
+    // Software pipeline: iteration kt issues tile kt+1's S^T MFMAs before
+    // tile kt's softmax, so the softmax VALU work overlaps matrix work.
+    f32x4 s[NQB][2];
+    if (wave_live && kt0 >= wkt0 && kt0 <= wkt1) tile_scores<NQB>(s, kbuf(kt0), koff0, koff1, qh, ql);
+    // the first iteration refills K tile kt0's slot: every wave must be done
+    // reading it
+    __syncthreads();
+
     for (int kt = kt0; kt <= kt1; kt++) {
-        const int nxt2 = cur == 0 ? 2 : cur - 1;    // stage of tile kt + 2 (= kt - 1's)
-        if (kt + 2 <= kt1) tile_fetch(smem + nxt2 * STAGEB, p, kvh, kt + 2, wave, lane);
-        const unsigned char *st = smem + cur * STAGEB;
+        // K of tile kt + 2 replaces K of tile kt (scored last iteration), V
+        // of tile kt + 1 replaces V of tile kt - 1
+        if (kt + 2 <= kt1) fetch_k<NW>(kbuf(kt + 2), kr, kt + 2, wave, lane);
+        if (kt + 1 <= kt1) fetch_vt(kt + 1);
+        const unsigned char *vs = vbuf(kt);
+
+        f32x4 sn[NQB][2];
+#pragma unroll
+        for (int b = 0; b < NQB; b++) sn[b][0] = s[b][0], sn[b][1] = s[b][1];
+        if (wave_live && kt + 1 >= wkt0 && kt + 1 <= wkt1)
+            tile_scores<NQB>(sn, kbuf(kt + 1), koff0, koff1, qh, ql);
 
         if (wave_live && kt >= wkt0 && kt <= wkt1) {
-            // ---- S^T = K . Q^T for keys 0-15 (s0) and 16-31 (s1), three fp16 passes ----
-            f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const half8 ah0 = *reinterpret_cast<const half8 *>(st + koff0 + 64 * t);
-                const half8 al0 = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * t);
-                const half8 ah1 = *reinterpret_cast<const half8 *>(st + koff1 + 64 * t);
-                const half8 al1 = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * t);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, qh[t], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, qh[t], s1, 0, 0, 0);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, ql[t], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, ql[t], s1, 0, 0, 0);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al0, qh[t], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al1, qh[t], s1, 0, 0, 0);
+            // the first V^T fragments load while the softmax runs
+            bf16x8 vf[3], vl[3];
+            vf[0] = *reinterpret_cast<const bf16x8 *>(vs + voff);
+            vf[1] = *reinterpret_cast<const bf16x8 *>(vs + voff + 1024);
+            if (VLO) {
+                vl[0] = *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff);
+                vl[1] = *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff + 1024);
             }
-            // register u of this lane: key kt*32 + 8 g + u (u < 4: s0[u], else s1[u-4])
-            float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-            // ---- mask (diagonal, window edge, ragged end) ----
             const bool edge = (kt * BK + BK - 1 > w_first) || (kt * BK <= w_last - p.window) ||
                               (kt * BK + BK > p.nk);
-            if (edge) {
+            bf16x8 ph[NQB], pl[NQB];
+#pragma unroll
+            for (int b = 0; b < NQB; b++) {
+                const int q_kk = p.hist + tok0 + 16 * b + ln;   // key index of this lane's query
+                // register u of this lane: key kt*32 + 8 g + u (u < 4: s[b][0][u], else s[b][1][u-4])
+                float sv[8] = {s[b][0][0], s[b][0][1], s[b][0][2], s[b][0][3],
+                               s[b][1][0], s[b][1][1], s[b][1][2], s[b][1][3]};
+                // ---- mask (diagonal, window edge, ragged end) ----
+                if (edge) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const int kk = kt * BK + 8 * g + u;
+                        const bool ok = kk <= q_kk && kk > q_kk - p.window && kk < p.nk;
+                        sv[u] = ok ? sv[u] : -INFINITY;
+                    }
+                }
+                // ---- online softmax with a lazy reference max ----
+                float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                                 fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const bool bump = mx > m_ref[b] + LAZY;
+                if (__builtin_amdgcn_ballot_w64(bump)) {
+                    const float m_new = bump ? mx : m_ref[b];
+                    const float alpha = fast_exp2(m_ref[b] - m_new);
+                    m_ref[b] = m_new;
+                    l_sum[b] *= alpha;
+#pragma unroll
+                    for (int mt = 0; mt < 16; mt++) o[b][mt] *= alpha;
+                }
+                float psum = 0.f;
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    const int kk = kt * BK + 8 * g + u;
-                    const bool ok = kk <= q_kk && kk > q_kk - p.window && kk < p.nk;
-                    sv[u] = ok ? sv[u] : -INFINITY;
+                    const float pr = fast_exp2(sv[u] - m_ref[b]);   // exp2(-inf) = 0 for masked keys
+                    psum += pr;
+                    const __bf16 hi = (__bf16)pr;
+                    ph[b][u] = hi;
+                    pl[b][u] = (__bf16)(pr - (float)hi);
                 }
+                psum += __shfl_xor(psum, 16);
+                psum += __shfl_xor(psum, 32);
+                l_sum[b] += psum;
             }
-            // ---- online softmax with a lazy reference max ----
-            float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                             fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const bool bump = mx > m_ref + LAZY;
-            if (__builtin_amdgcn_ballot_w64(bump)) {
-                const float m_new = bump ? mx : m_ref;
-                const float alpha = fast_exp2(m_ref - m_new);
-                m_ref = m_new;
-                l_sum *= alpha;
-#pragma unroll
-                for (int mt = 0; mt < 16; mt++) o[mt] *= alpha;
-            }
-            float psum = 0.f;
-            bf16x8 ph, pl;
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const float pr = fast_exp2(sv[u] - m_ref);   // exp2(-inf) = 0 for masked keys
-                psum += pr;
-                const __bf16 hi = (__bf16)pr;
-                ph[u] = hi;
-                pl[u] = (__bf16)(pr - (float)hi);
-            }
-            psum += __shfl_xor(psum, 16);
-            psum += __shfl_xor(psum, 32);
-            l_sum += psum;
-            // ---- O^T += V^T . P^T, two bf16 passes, 16 dim blocks ----
+            // ---- O^T += V^T . P^T over 16 dim blocks; the V^T fragments of
+            // block mt + 2 are read while block mt's MFMAs run ----
 #pragma unroll
             for (int mt = 0; mt < 16; mt++) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8 *>(st + voff + 1024 * mt);
-                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, ph, o[mt], 0, 0, 0);
-                o[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pl, o[mt], 0, 0, 0);
+                if (mt + 2 < 16) {
+                    vf[(mt + 2) % 3] = *reinterpret_cast<const bf16x8 *>(vs + voff + 1024 * (mt + 2));
+                    if (VLO)
+                        vl[(mt + 2) % 3] =
+                            *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff + 1024 * (mt + 2));
+                }
+                sched_fence();
+#pragma unroll
+                for (int b = 0; b < NQB; b++) {
+                    o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt % 3], ph[b], o[b][mt], 0, 0, 0);
+                    o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt % 3], pl[b], o[b][mt], 0, 0, 0);
+                    if (VLO)
+                        o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl[mt % 3], ph[b], o[b][mt], 0, 0, 0);
+                }
+                sched_fence();
             }
         }
+#pragma unroll
+        for (int b = 0; b < NQB; b++) s[b][0] = sn[b][0], s[b][1] = sn[b][1];
 
-        // tile kt + 1 must have landed before the barrier; kt + 2 may still fly
-        if (kt + 2 <= kt1) wait_fetch_but_one(); else wait_fetch_all();
+        // K of tile kt + 2 and V of tile kt + 1 must have landed before the
+        // barrier (next iteration's scores and P.V)
+        wait_fetch_all();
         __syncthreads();
-        cur = cur == 2 ? 0 : cur + 1;
     }
 
     // ---- normalise and write attn_out[token][qhead][dim] ----
-    if (!wave_live || tok >= p.n) return;
-    const float inv = 1.0f / l_sum;
-    float *orow = p.out + ((size_t)tok * p.n_kv_heads * G + qhead) * D + 4 * g;
+    if (!wave_live) return;
 #pragma unroll
-    for (int mt = 0; mt < 16; mt++)
-        *reinterpret_cast<float4 *>(orow + 16 * mt) =
-            make_float4(o[mt][0] * inv, o[mt][1] * inv, o[mt][2] * inv, o[mt][3] * inv);
+    for (int b = 0; b < NQB; b++) {
+        const int tok = tok0 + 16 * b + ln;
+        if (tok >= p.n) continue;
+        const float inv = 1.0f / l_sum[b];
+        float *orow = p.out + ((size_t)tok * p.n_kv_heads * G + qhead) * D + 4 * g;
+#pragma unroll
+        for (int mt = 0; mt < 16; mt++)
+            *reinterpret_cast<float4 *>(orow + 16 * mt) =
+                make_float4(o[b][mt][0] * inv, o[b][mt][1] * inv, o[b][mt][2] * inv, o[b][mt][3] * inv);
+    }
 }
 
-template <int G>
+// The V_lo pass is taken when this call's staging found a V that is not
+// exactly bf16 (flag == epoch); the branch is uniform over the grid.
+template <int G, int NQB>
+__global__ __launch_bounds__(512 / NQB, 1) void prefill_kernel(g3k_prefill_args p) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+    if (*p.v_lo_flag == p.epoch)
+        attend<G, NQB, true>(p, smem);
+    else
+        attend<G, NQB, false>(p, smem);
+}
+
+template <int G, int NQB>
 hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
-    constexpr int PB = 16 * (8 / G);
+    constexpr int PB = 16 * NQB * ((8 / NQB) / G);
     const int nqb = (a->n + PB - 1) / PB;
     // With timing events the dispatch itself records them (kernel begin / end).
-    hipExtLaunchKernelGGL(prefill_kernel<G>, dim3(nqb * a->n_kv_heads), dim3(NTA), 0, st,
+    hipExtLaunchKernelGGL((prefill_kernel<G, NQB>), dim3(nqb * a->n_kv_heads), dim3(512 / NQB), 0, st,
                           (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
     return hipGetLastError();
 }
@@ -346,7 +529,7 @@ hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
 
 extern "C" int g3k_stage(const g3k_stage_args *a, void *stream) {
     if (a->cnt <= 0) return 0;
-    if (a->ldk % 64 || a->kk0 + a->cnt > a->ldk) return (int)hipErrorInvalidValue;
+    if (a->ldk % 64 || a->kk0 + a->cnt > a->ldk || !a->v_lo_flag) return (int)hipErrorInvalidValue;
     dim3 grid((a->cnt + 63) / 64, D / 64, a->n_kv_heads);
     hipLaunchKernelGGL(stage_kernel, grid, dim3(NT), 0, (hipStream_t)stream, *a);
     return (int)hipGetLastError();
@@ -354,13 +537,17 @@ extern "C" int g3k_stage(const g3k_stage_args *a, void *stream) {
 
 extern "C" int g3k_prefill(const g3k_prefill_args *a, void *stream) {
     if (a->n <= 0) return 0;
-    if (a->ldk % 64 || a->nk > a->ldk || a->hist + a->n != a->nk || a->window < 1)
+    // buffer descriptors address one head's staging: ldk * 1 KiB must fit
+    // the 32-bit record count and the fetch offsets
+    if (a->ldk % 64 || a->ldk > (1LL << 20) || a->nk > a->ldk || a->hist + a->n != a->nk ||
+        a->window < 1 || !a->v_lo_flag)
         return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
+    const bool wide = a->queries_per_wave == 32;
     switch (a->group) {
-        case 1: return (int)launch_prefill<1>(a, st);
-        case 2: return (int)launch_prefill<2>(a, st);
-        case 4: return (int)launch_prefill<4>(a, st);
+        case 1: return (int)(wide ? launch_prefill<1, 2>(a, st) : launch_prefill<1, 1>(a, st));
+        case 2: return (int)(wide ? launch_prefill<2, 2>(a, st) : launch_prefill<2, 1>(a, st));
+        case 4: return (int)(wide ? launch_prefill<4, 2>(a, st) : launch_prefill<4, 1>(a, st));
         default: return (int)hipErrorInvalidValue;
     }
 }

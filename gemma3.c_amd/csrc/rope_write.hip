@@ -75,16 +75,16 @@ __global__ __launch_bounds__(256) void rope_write_kernel(g3k_rope_write_args a) 
         hi.y = a1 * t.w + b1 * t.z;
     }
 
-    if (kind == 1 && a.k_hi) {
-        // prefill staging: fp16 hi / lo split of the rotated key
+    if (kind == 1 && a.kq) {
+        // prefill staging: fp16 hi | lo row of the rotated key
         const _Float16 h0 = (_Float16)lo.x, h1 = (_Float16)lo.y, h2 = (_Float16)hi.x, h3 = (_Float16)hi.y;
         const _Float16 l0 = (_Float16)(lo.x - (float)h0), l1 = (_Float16)(lo.y - (float)h1);
         const _Float16 l2 = (_Float16)(hi.x - (float)h2), l3 = (_Float16)(hi.y - (float)h3);
-        const size_t o = ((size_t)h * a.ldk + a.row0 + i) * D;
-        *reinterpret_cast<uint32_t *>(a.k_hi + o + 2 * lane) = pack_f16(h0, h1);
-        *reinterpret_cast<uint32_t *>(a.k_hi + o + 128 + 2 * lane) = pack_f16(h2, h3);
-        *reinterpret_cast<uint32_t *>(a.k_lo + o + 2 * lane) = pack_f16(l0, l1);
-        *reinterpret_cast<uint32_t *>(a.k_lo + o + 128 + 2 * lane) = pack_f16(l2, l3);
+        uint16_t *row = a.kq + ((size_t)h * a.ldk + a.row0 + i) * (2 * D);
+        *reinterpret_cast<uint32_t *>(row + 2 * lane) = pack_f16(h0, h1);
+        *reinterpret_cast<uint32_t *>(row + 128 + 2 * lane) = pack_f16(h2, h3);
+        *reinterpret_cast<uint32_t *>(row + D + 2 * lane) = pack_f16(l0, l1);
+        *reinterpret_cast<uint32_t *>(row + D + 128 + 2 * lane) = pack_f16(l2, l3);
     }
     if (kind != 0 && i < a.kv_skip) return;
 

@@ -105,9 +105,13 @@ struct g3attn_ctx {
     /* grow-on-demand device buffers for host-pointer batch calls */
     void *d_big;
     size_t d_big_cap;
-    /* grow-on-demand prefill workspace (staged queries and keys) */
+    /* grow-on-demand prefill workspace (staged keys and values) */
     void *d_pf;
     size_t d_pf_cap;
+    /* prefill: staging sets *d_vflag = pf_epoch when a value is not exactly
+     * bf16 (the attention kernel then adds its V_lo pass) */
+    int *d_vflag;
+    int pf_epoch;
     /* kernel timing (g3attn_profile_*): event pairs per kind */
     struct {
         int on;
@@ -118,6 +122,7 @@ struct g3attn_ctx {
     } prof;
     int split_rows; /* 0 = heuristic */
     int min_rows;   /* smallest heuristic split */
+    int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
 };
 
@@ -150,6 +155,7 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_out);
     hipFree(c->d_big);
     hipFree(c->d_pf);
+    hipFree(c->d_vflag);
     if (c->h_in) hipHostFree(c->h_in);
     if (c->h_out) hipHostFree(c->h_out);
     if (c->stream) hipStreamDestroy(c->stream);
@@ -229,6 +235,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
     const size_t slots = ws_slots(cfg->num_kv_heads) * c->group;
     if (!alloc_dev((void **)&c->ws_acc, slots * D * sizeof(float), "decode workspace")) goto fail;
     if (!alloc_dev((void **)&c->ws_ml, slots * 2 * sizeof(float), "decode workspace")) goto fail;
+    if (!alloc_dev((void **)&c->d_vflag, sizeof(int), "prefill flag")) goto fail;
+    if (hipMemset(c->d_vflag, 0, sizeof(int)) != hipSuccess) goto fail_rt;
     {
         const char *w = getenv("G3ATTN_DECODE_WGS");
         const char *mr = getenv("G3ATTN_SPLIT_MIN_ROWS");
@@ -236,6 +244,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device);
         c->target_wgs = w ? atoi(w) : 2 * (cus > 0 ? cus : 256);
         c->min_rows = mr ? atoi(mr) : 64;
+        const char *qpw = getenv("G3ATTN_PREFILL_QPW");
+        c->prefill_qpw = (qpw && atoi(qpw) == 32) ? 32 : 16;
         if (c->min_rows < 64) c->min_rows = 64;
     }
 
@@ -606,8 +616,9 @@ int g3attn_kv_read(g3attn_ctx *c, int layer, int slot, int n, float *k_rows, flo
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-/* Grow-on-demand prefill workspace: q_out [H_q][n][D] fp32, k_hi / k_lo
- * [H_kv][ldk][D] fp16 and vt [H_kv][D][ldk] bf16. */
+/* Grow-on-demand prefill workspace: kq [H_kv][ldk][2][D] fp16 (hi | lo
+ * rows) and vt / vt_lo [H_kv][D][ldk] bf16 (the queries are normed and
+ * rotated inside the attention kernel, straight from the caller's Q). */
 static int grow_pf(g3attn_ctx *c, size_t bytes) {
     if (bytes <= c->d_pf_cap) return G3_OK;
     HIP_TRY(hipStreamSynchronize(c->stream), "grow prefill workspace");
@@ -642,16 +653,18 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     const int kstart = is_global ? 0 : (start_pos - W + 1 > 0 ? start_pos - W + 1 : 0);
     const int hist = start_pos - kstart, nk = hist + n;
     const long long ldk = ((long long)nk + 63) / 64 * 64;
-    const size_t q_bytes = align256((size_t)n * Hq * D * sizeof(float));
-    const size_t k_bytes = align256((size_t)Hkv * ldk * D * sizeof(uint16_t));
+    const size_t v_bytes = align256((size_t)Hkv * ldk * D * sizeof(uint16_t));
     hipSetDevice(c->device);
-    int rc = grow_pf(c, q_bytes + 3 * k_bytes);
+    int rc = grow_pf(c, 4 * v_bytes);
     if (rc) return rc;
     unsigned char *ws = (unsigned char *)c->d_pf;
-    float *q_out = (float *)ws;
-    uint16_t *k_hi = (uint16_t *)(ws + q_bytes);
-    uint16_t *k_lo = (uint16_t *)(ws + q_bytes + k_bytes);
-    uint16_t *vt = (uint16_t *)(ws + q_bytes + 2 * k_bytes);
+    uint16_t *kq = (uint16_t *)ws;
+    uint16_t *vt = (uint16_t *)(ws + 2 * v_bytes);
+    uint16_t *vt_lo = (uint16_t *)(ws + 3 * v_bytes);
+    /* a fresh epoch per call: a flag left by an earlier call never matches */
+    c->pf_epoch = c->pf_epoch >= INT_MAX - 1 ? 1 : c->pf_epoch + 1;
+    const int norm = q_norm && k_norm;
+    const float *rope = is_global ? c->rope_global : c->rope_local;
     const long long head_stride = (long long)c->rows[layer] * D;
 
     /* 1. history keys, read from the cache before this batch's ring writes */
@@ -669,42 +682,43 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
         sa.cnt = hist;
         sa.nk = nk;
         sa.n_kv_heads = Hkv;
-        sa.k_hi = k_hi;
-        sa.k_lo = k_lo;
+        sa.kq = kq;
         sa.vt = vt;
+        sa.vt_lo = vt_lo;
         sa.ldk = ldk;
+        sa.v_lo_flag = c->d_vflag;
+        sa.epoch = c->pf_epoch;
         rc = g3k_stage(&sa, c->stream);
         if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill stage");
     }
-    /* 2. QK-norm + RoPE of the batch, cache_kv, fp16 split keys
-     *    (gemma3_transformer.c:650-671 for every token) */
+    /* 2. K-norm + RoPE of the batch, cache_kv, fp16 split keys
+     *    (the key half of gemma3_transformer.c:650-671 for every token) */
     g3k_rope_write_args ra;
     memset(&ra, 0, sizeof ra);
-    ra.Q = Q;
+    ra.Q = NULL;
     ra.K = K;
     ra.V = V;
-    ra.q_norm = (q_norm && k_norm) ? q_norm : NULL;
-    ra.k_norm = (q_norm && k_norm) ? k_norm : NULL;
-    ra.rope = is_global ? c->rope_global : c->rope_local;
+    ra.q_norm = norm ? q_norm : NULL;
+    ra.k_norm = norm ? k_norm : NULL;
+    ra.rope = rope;
     ra.eps = c->cfg.rmsnorm_eps;
     ra.n = n;
     ra.start_pos = start_pos;
     ra.n_heads = Hq;
     ra.n_kv_heads = Hkv;
-    ra.q_out = q_out;
+    ra.q_out = NULL;
     ra.k_dst = c->kc[layer];
     ra.v_dst = c->vc[layer];
     ra.dst_head_stride = head_stride;
     ra.ring = is_global ? 0 : W;
     ra.dst_pos0 = 0;
     ra.kv_skip = (!is_global && n > W) ? n - W : 0;
-    ra.k_hi = k_hi;
-    ra.k_lo = k_lo;
+    ra.kq = kq;
     ra.ldk = ldk;
     ra.row0 = hist;
     rc = g3k_rope_write(&ra, c->stream);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill rope");
-    /* 3. the batch's values as bf16 V^T, and zeroed padding up to ldk */
+    /* 3. the batch's values as bf16 hi / lo V^T, and zeroed padding up to ldk */
     {
         g3k_stage_args sa;
         memset(&sa, 0, sizeof sa);
@@ -719,20 +733,29 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
         sa.cnt = (int)(ldk - hist);
         sa.nk = nk;
         sa.n_kv_heads = Hkv;
-        sa.k_hi = k_hi;
-        sa.k_lo = k_lo;
+        sa.kq = kq;
         sa.vt = vt;
+        sa.vt_lo = vt_lo;
         sa.ldk = ldk;
+        sa.v_lo_flag = c->d_vflag;
+        sa.epoch = c->pf_epoch;
         rc = g3k_stage(&sa, c->stream);
         if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill stage");
     }
-    /* 4. attention (gemma3_gqa for every token, gemma3_transformer.c:673-691) */
+    /* 4. Q-norm + RoPE and attention (gemma3_transformer.c:650-667 for the
+     *    queries, gemma3_gqa for every token, :673-691) */
     g3k_prefill_args pa;
     memset(&pa, 0, sizeof pa);
-    pa.q = q_out;
-    pa.k_hi = k_hi;
-    pa.k_lo = k_lo;
+    pa.q = Q;
+    pa.q_norm = norm ? q_norm : NULL;
+    pa.rope = rope;
+    pa.eps = c->cfg.rmsnorm_eps;
+    pa.start_pos = start_pos;
+    pa.kq = kq;
     pa.vt = vt;
+    pa.vt_lo = vt_lo;
+    pa.v_lo_flag = c->d_vflag;
+    pa.epoch = c->pf_epoch;
     pa.out = attn_out;
     pa.ldk = ldk;
     pa.n = n;
@@ -742,6 +765,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.n_kv_heads = Hkv;
     pa.group = c->group;
     pa.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
+    pa.queries_per_wave = c->prefill_qpw;
     rc = prof_slot(c, 1, &pa.ev0, &pa.ev1);
     if (rc) return rc;
     rc = g3k_prefill(&pa, c->stream);

@@ -40,7 +40,10 @@ constexpr int NT = 256;               // threads per workgroup
 constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
 // one row so its larger q / acc arrays fit without spills.
-template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
+#ifndef G3K_DEC_R
+#define G3K_DEC_R 2
+#endif
+template <int G> constexpr int rows_for() { return G >= 4 ? 1 : G3K_DEC_R; }
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
 // in flight per wave, one contiguous row range per split.  Double-buffered
@@ -172,8 +175,7 @@ __device__ __forceinline__ void step_compute(const float (&kk)[R][4][4], const f
         float mx = s[g][0];
 #pragma unroll
         for (int r = 1; r < R; r++) mx = fmaxf(mx, s[g][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = col4_max(mx);
         const float mn = fmaxf(m[g], mx);
         const float alpha = fast_exp2(m[g] - mn);
         m[g] = mn;
@@ -290,15 +292,13 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     // ---- merge the four lane-groups of each wave (they share m) ----
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        l[g] += __shfl_xor(l[g], 16);
-        l[g] += __shfl_xor(l[g], 32);
+        l[g] = col4_sum(l[g]);
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 float a = acc[g][j][e];
-                a += __shfl_xor(a, 16);
-                a += __shfl_xor(a, 32);
+                a = col4_sum(a);
                 acc[g][j][e] = a;
             }
     }
@@ -346,62 +346,90 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
 }
 
 // Cross-split combine, one launch after decode_kernel (kernel order makes
-// the partials visible; no fences or atomics).  grid (D / 64, group, H_kv),
-// 256 threads: wave w takes splits w, w+4, ...; lane l owns dim 64*x + l.
+// the partials visible; no fences or atomics).  grid (D / 32, group, H_kv),
+// 256 threads: lane f = t % 8 owns dims 32 x + 4 f .. + 3, split lane
+// t / 8 takes splits t / 8 + 32 u.  Every partial a thread needs is loaded
+// at once (one memory round trip), merged in registers, then across the 8
+// split lanes of a wave by shuffles and across the 4 waves through LDS.
+constexpr int CMB_SL = NT / 8;                     // split lanes per workgroup
+constexpr int CMB_U = G3K_MAX_SPLITS / CMB_SL;     // splits per thread, at most
+
+// (M, L, A) <- merge of two online-softmax partials
+__device__ __forceinline__ void merge_ml(float &M, float &L, float4 &A, float m2, float l2, float4 a2) {
+    const float Mn = fmaxf(M, m2);
+    const float f1 = fast_exp2(M - Mn), f2 = fast_exp2(m2 - Mn);
+    L = L * f1 + l2 * f2;
+    A.x = A.x * f1 + a2.x * f2;
+    A.y = A.y * f1 + a2.y * f2;
+    A.z = A.z * f1 + a2.z * f2;
+    A.w = A.w * f1 + a2.w * f2;
+    M = Mn;
+}
+
 template <int G>
 __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
     const int x = blockIdx.x, g = blockIdx.y, kvh = blockIdx.z;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int d = 64 * x + lane;
-    __shared__ float s_a[NW][64], s_m[NW], s_l[NW];
+    const int f = tid & 7, sl = tid >> 3;
+    const int d = 32 * x + 4 * f;
     const int S = p.n_splits;
     const size_t slot0 = (size_t)kvh * G3K_MAX_SPLITS;
-    // One pass: batches of CB splits are loaded together (no load depends on
-    // the math) and merged into a running (M, L, A) with online rescaling.
-    constexpr int CB = 8;
-    float M = NEG_BIG, L = 0.f, A = 0.f;
-    for (int q0 = wave; q0 < S; q0 += NW * CB) {
-        float mq[CB], lq[CB], aq[CB];
+    float mq[CMB_U], lq[CMB_U];
+    float4 aq[CMB_U];
 #pragma unroll
-        for (int u = 0; u < CB; u++) {
-            const int q = q0 + u * NW;
-            const size_t sl = (slot0 + (q < S ? q : q0)) * G + g;
-            mq[u] = q < S ? p.ws_ml[sl * 2] : NEG_BIG;
-            lq[u] = p.ws_ml[sl * 2 + 1];
-            aq[u] = p.ws_acc[sl * D + d];
+    for (int u = 0; u < CMB_U; u++) {
+        const int q = sl + CMB_SL * u;
+        if (q < S) {
+            const size_t sg = (slot0 + q) * G + g;
+            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + sg * 2);
+            mq[u] = ml.x;
+            lq[u] = ml.y;
+            aq[u] = *reinterpret_cast<const float4 *>(p.ws_acc + sg * D + d);
+        } else {
+            mq[u] = NEG_BIG;
+            lq[u] = 0.f;
+            aq[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        float Mn = M;
-#pragma unroll
-        for (int u = 0; u < CB; u++) Mn = fmaxf(Mn, mq[u]);
-        const float r = fast_exp2(M - Mn);
-        L *= r;
-        A *= r;
-#pragma unroll
-        for (int u = 0; u < CB; u++) {
-            const float b = (q0 + u * NW < S) ? fast_exp2(mq[u] - Mn) : 0.f;
-            L += lq[u] * b;
-            A += aq[u] * b;
-        }
-        M = Mn;
     }
-    s_a[wave][lane] = A;
-    if (lane == 0) {
-        s_m[wave] = M;
-        s_l[wave] = L;
+    float M = NEG_BIG;
+#pragma unroll
+    for (int u = 0; u < CMB_U; u++) M = fmaxf(M, mq[u]);
+    float L = 0.f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < CMB_U; u++) {
+        const float b = fast_exp2(mq[u] - M);
+        L += lq[u] * b;
+        A.x += aq[u].x * b;
+        A.y += aq[u].y * b;
+        A.z += aq[u].z * b;
+        A.w += aq[u].w * b;
+    }
+    // the 8 split lanes of this wave: lanes f + 8 k
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) {
+        const float m2 = __shfl_xor(M, o), l2 = __shfl_xor(L, o);
+        float4 a2;
+        a2.x = __shfl_xor(A.x, o);
+        a2.y = __shfl_xor(A.y, o);
+        a2.z = __shfl_xor(A.z, o);
+        a2.w = __shfl_xor(A.w, o);
+        merge_ml(M, L, A, m2, l2, a2);
+    }
+    __shared__ float s_m[NW][8], s_l[NW][8];
+    __shared__ float4 s_a[NW][8];
+    if (lane < 8) {
+        s_m[wave][lane] = M;
+        s_l[wave][lane] = L;
+        s_a[wave][lane] = A;
     }
     __syncthreads();
-    if (wave == 0) {
-        float Mx = s_m[0];
+    if (tid < 8) {
 #pragma unroll
-        for (int w = 1; w < NW; w++) Mx = fmaxf(Mx, s_m[w]);
-        float Lx = 0.f, Ax = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float f = fast_exp2(s_m[w] - Mx);
-            Lx += s_l[w] * f;
-            Ax += s_a[w][lane] * f;
-        }
-        p.out[((size_t)kvh * G + g) * D + d] = Ax / Lx;
+        for (int w = 1; w < NW; w++) merge_ml(M, L, A, s_m[w][tid], s_l[w][tid], s_a[w][tid]);
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4 *>(p.out + ((size_t)kvh * G + g) * D + d) =
+            make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
     }
 }
 
@@ -413,7 +441,7 @@ hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
                           (hipEvent_t)a->ev1, 0, *a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a->n_splits == 1) return e;
-    hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 64, G, a->n_kv_heads), dim3(NT), 0, st, *a);
+    hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 32, G, a->n_kv_heads), dim3(NT), 0, st, *a);
     return hipGetLastError();
 }
 

@@ -132,6 +132,7 @@ typedef struct {
     int n_kv_heads, group;
     float qscale;             /* softmax scale * log2(e) */
     int queries_per_wave;     /* 16 (8 waves, 2 per SIMD) or 32 (4 waves, 1 per SIMD) */
+    int schedule;             /* 16 queries per wave: 0 = all waves in phase, 1 = SIMD pairs in opposite phase */
     void *ev0, *ev1;          /* hipEvent_t: begin / end of prefill_kernel's dispatch, or NULL */
 } g3k_prefill_args;
 

@@ -21,13 +21,32 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Sum over all 64 lanes; every lane gets the total.
-__device__ __forceinline__ float wave_sum(float v) {
-    v = row16_sum(v);
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+// gfx950 v_permlane32_swap / v_permlane16_swap with both operands = v: the
+// two results hold v of lanes {l, l ^ 32} (resp. {l, l ^ 16}) in some order,
+// so their sum / max is the pair's.  VALU only, no LDS round trip.
+__device__ __forceinline__ float pair32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+__device__ __forceinline__ float pair16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Sum / max over the four lanes l % 16 + 16 g (g = 0..3); every lane gets it.
+__device__ __forceinline__ float col4_sum(float v) { return pair16_sum(pair32_sum(v)); }
+__device__ __forceinline__ float col4_max(float v) { return pair16_max(pair32_max(v)); }
+
+// Sum over all 64 lanes; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) { return col4_sum(row16_sum(v)); }
 
 // v_exp_f32: 2^x, flushes to 0 for very negative x.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

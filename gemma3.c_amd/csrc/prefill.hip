@@ -67,6 +67,9 @@ constexpr int LDS_V0 = 2 * KTILEB;           // V ring after the K ring
 constexpr int LDS_BYTES = LDS_V0 + 2 * 2 * VTILEB;   // 132096
 constexpr float NEG_BIG = -1.0e30f;
 constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
+#ifndef G3K_KPF
+#define G3K_KPF 1                            // K fragment prefetch depth (d-steps)
+#endif
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -219,22 +222,22 @@ template <int NQB>
 __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned char *st, int koff0,
                                             int koff1, const half8 (&qh)[NQB][8],
                                             const half8 (&ql)[NQB][8]) {
+    constexpr int PF = G3K_KPF;       // d-steps of K fragments in flight
 #pragma unroll
     for (int b = 0; b < NQB; b++) s[b][0] = s[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    half8 f[2][4];
-    f[0][0] = *reinterpret_cast<const half8 *>(st + koff0);
-    f[0][1] = *reinterpret_cast<const half8 *>(st + koff0 + 512);
-    f[0][2] = *reinterpret_cast<const half8 *>(st + koff1);
-    f[0][3] = *reinterpret_cast<const half8 *>(st + koff1 + 512);
+    half8 f[PF + 1][4];
+    auto load = [&](half8 (&r)[4], int t) {
+        r[0] = *reinterpret_cast<const half8 *>(st + koff0 + 64 * t);
+        r[1] = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * t);
+        r[2] = *reinterpret_cast<const half8 *>(st + koff1 + 64 * t);
+        r[3] = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * t);
+    };
+#pragma unroll
+    for (int t = 0; t < PF; t++) load(f[t], t);
 #pragma unroll
     for (int t = 0; t < 8; t++) {
-        const int c = t & 1, n = c ^ 1;
-        if (t < 7) {
-            f[n][0] = *reinterpret_cast<const half8 *>(st + koff0 + 64 * (t + 1));
-            f[n][1] = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * (t + 1));
-            f[n][2] = *reinterpret_cast<const half8 *>(st + koff1 + 64 * (t + 1));
-            f[n][3] = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * (t + 1));
-        }
+        const int c = t % (PF + 1);
+        if (t + PF < 8) load(f[(t + PF) % (PF + 1)], t + PF);
         sched_fence();
 #pragma unroll
         for (int b = 0; b < NQB; b++) {
@@ -271,8 +274,7 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
         for (int t = 0; t < 8; t++)
 #pragma unroll
             for (int u = 0; u < 8; u++) ss += x[t][u] * x[t][u];
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
+        ss = col4_sum(ss);
         const float r = 1.0f / sqrtf(ss / (float)D + p.eps);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
@@ -329,6 +331,9 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     const int qhead = kvh * G + wave / WPH;
     const int tok0 = qb * PB + (wave % WPH) * QW;
     const bool wave_live = tok0 < p.n;
+    // waves w and w + 4 share a SIMD; with schedule 1 the upper four run each
+    // tile's softmax + P.V before the next tile's scores
+    const bool late = NW == 8 && ((p.schedule == 1 && (wave >> 2) == 1) || (p.schedule == 2 && (wave & 1)));
 
     // key index range of the workgroup and of this wave (inclusive)
     const int wg_first = p.hist + qb * PB;
@@ -384,8 +389,8 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     wait_fetch_all();
     __syncthreads();
 
-    // Software pipeline: iteration kt issues tile kt+1's S^T MFMAs before
-    // tile kt's softmax, so the softmax VALU work overlaps matrix work.
+    // Software pipeline: iteration kt issues tile kt+1's S^T MFMAs and tile
+    // kt's softmax + P.V (in either order, see `late`).
     f32x4 s[NQB][2];
     if (wave_live && kt0 >= wkt0 && kt0 <= wkt1) tile_scores<NQB>(s, kbuf(kt0), koff0, koff1, qh, ql);
     // the first iteration refills K tile kt0's slot: every wave must be done
@@ -402,10 +407,12 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         f32x4 sn[NQB][2];
 #pragma unroll
         for (int b = 0; b < NQB; b++) sn[b][0] = s[b][0], sn[b][1] = s[b][1];
-        if (wave_live && kt + 1 >= wkt0 && kt + 1 <= wkt1)
-            tile_scores<NQB>(sn, kbuf(kt + 1), koff0, koff1, qh, ql);
-
-        if (wave_live && kt >= wkt0 && kt <= wkt1) {
+        auto scores_next = [&]() {
+            if (wave_live && kt + 1 >= wkt0 && kt + 1 <= wkt1)
+                tile_scores<NQB>(sn, kbuf(kt + 1), koff0, koff1, qh, ql);
+        };
+        auto softmax_pv = [&]() {
+          if (wave_live && kt >= wkt0 && kt <= wkt1) {
             // the first V^T fragments load while the softmax runs
             bf16x8 vf[3], vl[3];
             vf[0] = *reinterpret_cast<const bf16x8 *>(vs + voff);
@@ -435,8 +442,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
                 // ---- online softmax with a lazy reference max ----
                 float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                                  fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = col4_max(mx);
                 const bool bump = mx > m_ref[b] + LAZY;
                 if (__builtin_amdgcn_ballot_w64(bump)) {
                     const float m_new = bump ? mx : m_ref[b];
@@ -455,9 +461,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
                     ph[b][u] = hi;
                     pl[b][u] = (__bf16)(pr - (float)hi);
                 }
-                psum += __shfl_xor(psum, 16);
-                psum += __shfl_xor(psum, 32);
-                l_sum[b] += psum;
+                l_sum[b] += psum;   // this lane's keys; the four lanes add up at the end
             }
             // ---- O^T += V^T . P^T over 16 dim blocks; the V^T fragments of
             // block mt + 2 are read while block mt's MFMAs run ----
@@ -479,6 +483,16 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
                 }
                 sched_fence();
             }
+          }
+        };
+        // The two waves of a SIMD run the phases in opposite order, so one's
+        // softmax (VALU) overlaps the other's matrix work.
+        if (late) {
+            softmax_pv();
+            scores_next();
+        } else {
+            scores_next();
+            softmax_pv();
         }
 #pragma unroll
         for (int b = 0; b < NQB; b++) s[b][0] = sn[b][0], s[b][1] = sn[b][1];
@@ -493,9 +507,9 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     if (!wave_live) return;
 #pragma unroll
     for (int b = 0; b < NQB; b++) {
+        const float inv = 1.0f / col4_sum(l_sum[b]);   // all lanes active here
         const int tok = tok0 + 16 * b + ln;
         if (tok >= p.n) continue;
-        const float inv = 1.0f / l_sum[b];
         float *orow = p.out + ((size_t)tok * p.n_kv_heads * G + qhead) * D + 4 * g;
 #pragma unroll
         for (int mt = 0; mt < 16; mt++)

@@ -123,6 +123,7 @@ struct g3attn_ctx {
     int split_rows; /* 0 = heuristic */
     int min_rows;   /* smallest heuristic split */
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
+    int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
 };
 
@@ -246,6 +247,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         c->min_rows = mr ? atoi(mr) : 64;
         const char *qpw = getenv("G3ATTN_PREFILL_QPW");
         c->prefill_qpw = (qpw && atoi(qpw) == 32) ? 32 : 16;
+        const char *sch = getenv("G3ATTN_PREFILL_SCHED");
+        c->prefill_sched = sch ? atoi(sch) : 1;
         if (c->min_rows < 64) c->min_rows = 64;
     }
 
@@ -766,6 +769,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.group = c->group;
     pa.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
     pa.queries_per_wave = c->prefill_qpw;
+    pa.schedule = c->prefill_sched;
     rc = prof_slot(c, 1, &pa.ev0, &pa.ev1);
     if (rc) return rc;
     rc = g3k_prefill(&pa, c->stream);

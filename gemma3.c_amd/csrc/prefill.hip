@@ -322,6 +322,9 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     constexpr int PB = QW * WPH;      // query positions per workgroup
     constexpr int VST = VTILEB * (VLO ? 2 : 1);   // V ring slot: hi (| lo)
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // The wave index is uniform per wave; saying so for the fetches keeps
+    // their offsets and LDS addresses in SGPRs (no per-lane loop around each).
+    const int fwave = __builtin_amdgcn_readfirstlane(wave);
     const int g = lane >> 4, ln = lane & 15;     // lane group, query column
     // 1-D grid, longest (latest) query blocks first across all heads: with
     // workgroups dealt round-robin to the 8 XCDs, block id -> (qb, id % H_kv)
@@ -354,14 +357,14 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     auto kbuf = [&](int kt) { return smem + (kt & 1) * KTILEB; };
     auto vbuf = [&](int kt) { return smem + LDS_V0 + (kt & 1) * VST; };
     auto fetch_vt = [&](int kt) {
-        fetch_v<NW>(vbuf(kt), vr, kt, wave, voff_v, ldk);
-        if (VLO) fetch_v<NW>(vbuf(kt) + VTILEB, vlr, kt, wave, voff_v, ldk);
+        fetch_v<NW>(vbuf(kt), vr, kt, fwave, voff_v, ldk);
+        if (VLO) fetch_v<NW>(vbuf(kt) + VTILEB, vlr, kt, fwave, voff_v, ldk);
     };
 
     // ---- K of the first two tiles and V of the first in flight, then this
     // wave's queries ----
-    fetch_k<NW>(kbuf(kt0), kr, kt0, wave, lane);
-    if (kt0 + 1 <= kt1) fetch_k<NW>(kbuf(kt0 + 1), kr, kt0 + 1, wave, lane);
+    fetch_k<NW>(kbuf(kt0), kr, kt0, fwave, lane);
+    if (kt0 + 1 <= kt1) fetch_k<NW>(kbuf(kt0 + 1), kr, kt0 + 1, fwave, lane);
     fetch_vt(kt0);
 
     half8 qh[NQB][8], ql[NQB][8];
@@ -400,7 +403,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     for (int kt = kt0; kt <= kt1; kt++) {
         // K of tile kt + 2 replaces K of tile kt (scored last iteration), V
         // of tile kt + 1 replaces V of tile kt - 1
-        if (kt + 2 <= kt1) fetch_k<NW>(kbuf(kt + 2), kr, kt + 2, wave, lane);
+        if (kt + 2 <= kt1) fetch_k<NW>(kbuf(kt + 2), kr, kt + 2, fwave, lane);
         if (kt + 1 <= kt1) fetch_vt(kt + 1);
         const unsigned char *vs = vbuf(kt);
 

@@ -459,7 +459,7 @@ int capacity() {
 
 extern "C" int g3k_decode(const g3k_decode_args *a, int fused, void *stream) {
     hipStream_t st = (hipStream_t)stream;
-    if (a->n_splits < 1 || a->n_splits > G3K_MAX_SPLITS || a->rows_per_split % 64)
+    if (a->n_splits < 1 || a->n_splits > G3K_MAX_SPLITS || a->rows_per_split % G3K_SPLIT_GRAIN)
         return (int)hipErrorInvalidValue;
     switch (a->group) {
         case 1: return (int)(fused ? launch<1, true>(a, st) : launch<1, false>(a, st));

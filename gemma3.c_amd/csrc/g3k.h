@@ -22,6 +22,7 @@ extern "C" {
 
 #define G3K_HEAD_DIM 256
 #define G3K_MAX_SPLITS 256
+#define G3K_SPLIT_GRAIN 32   /* decode split granularity (rows): one workgroup step at group <= 2 */
 
 typedef struct {
     /* query side */
@@ -40,7 +41,7 @@ typedef struct {
     int new_slot;          /* cache row receiving the new k/v (fused decode) */
     const float *mask;     /* additive mask per attention index or NULL (gqa) */
     float qscale;          /* softmax scale * log2(e) */
-    int rows_per_split;    /* multiple of 64 */
+    int rows_per_split;    /* multiple of G3K_SPLIT_GRAIN */
     int n_splits;          /* <= G3K_MAX_SPLITS */
     int n_kv_heads;
     int group;             /* query heads per kv head: 1, 2 or 4 */

@@ -244,12 +244,12 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         int cus = 0;
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device);
         c->target_wgs = w ? atoi(w) : 2 * (cus > 0 ? cus : 256);
-        c->min_rows = mr ? atoi(mr) : 64;
+        c->min_rows = mr ? atoi(mr) : G3K_SPLIT_GRAIN;
         const char *qpw = getenv("G3ATTN_PREFILL_QPW");
         c->prefill_qpw = (qpw && atoi(qpw) == 32) ? 32 : 16;
         const char *sch = getenv("G3ATTN_PREFILL_SCHED");
         c->prefill_sched = sch ? atoi(sch) : 1;
-        if (c->min_rows < 64) c->min_rows = 64;
+        if (c->min_rows < G3K_SPLIT_GRAIN) c->min_rows = G3K_SPLIT_GRAIN;
     }
 
     const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D;
@@ -385,12 +385,12 @@ int g3attn_profile_read(g3attn_ctx *c, int kind, double *total_ms, int *count) {
 
 /* Split-K shape: target_wgs workgroups (default two per compute unit,
  * G3ATTN_DECODE_WGS overrides) spread over the KV heads, rows per split a
- * multiple of 64 and at least min_rows (G3ATTN_SPLIT_MIN_ROWS, default 64),
- * at most G3K_MAX_SPLITS splits per head. */
+ * multiple of G3K_SPLIT_GRAIN and at least min_rows (G3ATTN_SPLIT_MIN_ROWS,
+ * default one grain), at most G3K_MAX_SPLITS splits per head. */
 static void choose_splits(int n_stream, int n_kv, int target_wgs, int override_rows,
                           int min_rows, g3k_decode_args *a) {
     if (n_stream <= 0) {
-        a->rows_per_split = 64;
+        a->rows_per_split = G3K_SPLIT_GRAIN;
         a->n_splits = 1;
         return;
     }
@@ -398,11 +398,11 @@ static void choose_splits(int n_stream, int n_kv, int target_wgs, int override_r
     if (per_head < 1) per_head = 1;
     long r = override_rows > 0 ? override_rows : (n_stream + per_head - 1) / per_head;
     if (override_rows <= 0 && r < min_rows) r = min_rows;
-    r = (r + 63) / 64 * 64;
+    r = (r + G3K_SPLIT_GRAIN - 1) / G3K_SPLIT_GRAIN * G3K_SPLIT_GRAIN;
     long s = (n_stream + r - 1) / r;
     if (s > G3K_MAX_SPLITS) {
         r = ((long)n_stream + G3K_MAX_SPLITS - 1) / G3K_MAX_SPLITS;
-        r = (r + 63) / 64 * 64;
+        r = (r + G3K_SPLIT_GRAIN - 1) / G3K_SPLIT_GRAIN * G3K_SPLIT_GRAIN;
         s = (n_stream + r - 1) / r;
     }
     a->rows_per_split = (int)r;

@@ -139,6 +139,22 @@ typedef struct {
 
 int g3k_prefill(const g3k_prefill_args *a, void *stream);
 
+/* bf16-weight GEMV, y[m] = A[m] . x for up to G3K_MATVEC_MAX matrices that
+ * share x (one launch): A[m] [M[m]][K] bf16 row-major, x [K], y[m] [M[m]]
+ * fp32.  K <= G3K_MATVEC_MAX_K (x is staged in LDS). */
+#define G3K_MATVEC_MAX 3
+#define G3K_MATVEC_MAX_K 40960
+typedef struct {
+    const float *x;
+    int K;
+    int n_mat;
+    const uint16_t *A[G3K_MATVEC_MAX];
+    float *y[G3K_MATVEC_MAX];
+    int M[G3K_MATVEC_MAX];
+} g3k_matvec_args;
+
+int g3k_matvec(const g3k_matvec_args *a, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,149 @@
+// matvec.hip - bf16-weight GEMV y = A . x on gfx950, for the projections on
+// either side of the attention block.
+//
+// Replaces gemma3_matvec_bf16 (gemma3_kernels.h:217-218, gemma3_kernels.c:
+// 188-238): A is [M][K] bf16 row-major, x and y fp32, y[i] = sum_k
+// bf16(A[i][k]) * x[k] accumulated in fp32 (the reference's scalar / AVX2
+// loops; the summation order differs, which the parity tests bound).
+// Callers: layer_attention's Q/K/V projections (gemma3_transformer.c:290-292)
+// and its output projection (:355).
+//
+// At decode batch 1 the GEMV is HBM-bound: 2 bytes of A per multiply-add.
+// Workgroup = 4 waves; each wave owns RPW consecutive rows.  Lane l reads the
+// 16-byte chunks 8 l + 512 j of each row, so one wave load covers 1 KiB of a
+// row, contiguous, and all of a row's loads are issued before the FMAs that
+// use them.  x is staged once per workgroup in LDS.  Row sums reduce over the
+// wave with DPP and permlane swaps.  Rows whose length is not a multiple of 8
+// (or unaligned buffers) take a lane-strided scalar path.
+//
+// One launch can serve up to three matrices that share x (the Q, K and V
+// projections of one token): workgroups are dealt to the matrices in order of
+// their row blocks.
+#include <hip/hip_runtime.h>
+
+#include "g3k.h"
+#include "g3k_device.h"
+
+namespace {
+
+using namespace g3k;
+
+constexpr int NT = 256;   // 4 waves
+constexpr int NW = NT / 64;
+
+__device__ __forceinline__ float dot8(uint4 w, float4 xa, float4 xb) {
+    float s = bf16f(w.x & 0xffff) * xa.x;
+    s = fmaf(bf16f(w.x >> 16), xa.y, s);
+    s = fmaf(bf16f(w.y & 0xffff), xa.z, s);
+    s = fmaf(bf16f(w.y >> 16), xa.w, s);
+    s = fmaf(bf16f(w.z & 0xffff), xb.x, s);
+    s = fmaf(bf16f(w.z >> 16), xb.y, s);
+    s = fmaf(bf16f(w.w & 0xffff), xb.z, s);
+    s = fmaf(bf16f(w.w >> 16), xb.w, s);
+    return s;
+}
+
+// Matrix m of the launch and the workgroup's first row in it.
+__device__ __forceinline__ int pick(const g3k_matvec_args &a, int rows_per_wg, int &row0) {
+    int b = blockIdx.x;
+    for (int m = 0; m < a.n_mat; m++) {
+        const int nb = (a.M[m] + rows_per_wg - 1) / rows_per_wg;
+        if (b < nb) {
+            row0 = b * rows_per_wg;
+            return m;
+        }
+        b -= nb;
+    }
+    row0 = 0;
+    return -1;
+}
+
+template <int RPW, bool VEC>
+__global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
+    extern __shared__ float xs[];
+    const int K = a.K;
+    int row0;
+    const int m = pick(a, NW * RPW, row0);
+    if (m < 0) return;   // uniform over the workgroup
+    for (int i = threadIdx.x; i < K; i += NT) xs[i] = a.x[i];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int M = a.M[m];
+    const uint16_t *A = a.A[m];
+    const int r0 = row0 + wave * RPW;
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) acc[r] = 0.f;
+
+    if (VEC) {
+        // 16-byte chunks: chunk c covers elements 8c .. 8c + 7; lane l takes
+        // chunks l, l + 64, ...; four chunks per row are loaded ahead
+        const int nch = K >> 3;
+        constexpr int U = 4;
+        for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+            uint4 w[RPW][U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = c0 + 64 * u;
+#pragma unroll
+                for (int r = 0; r < RPW; r++) {
+                    const int row = r0 + r < M ? r0 + r : M - 1;
+                    w[r][u] = c < nch ? *reinterpret_cast<const uint4 *>(A + (size_t)row * K + 8 * c)
+                                      : make_uint4(0, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = c0 + 64 * u;
+                if (c < nch) {
+                    const float4 xa = *reinterpret_cast<const float4 *>(xs + 8 * c);
+                    const float4 xb = *reinterpret_cast<const float4 *>(xs + 8 * c + 4);
+#pragma unroll
+                    for (int r = 0; r < RPW; r++) acc[r] += dot8(w[r][u], xa, xb);
+                }
+            }
+        }
+    } else {
+        for (int k = lane; k < K; k += 64) {
+            const float xv = xs[k];
+#pragma unroll
+            for (int r = 0; r < RPW; r++) {
+                const int row = r0 + r < M ? r0 + r : M - 1;
+                acc[r] = fmaf(bf16f(A[(size_t)row * K + k]), xv, acc[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const float s = wave_sum(acc[r]);
+        if (lane == 0 && r0 + r < M) a.y[m][r0 + r] = s;
+    }
+}
+
+template <int RPW, bool VEC>
+hipError_t launch(const g3k_matvec_args *a, hipStream_t st) {
+    int blocks = 0;
+    for (int m = 0; m < a->n_mat; m++) blocks += (a->M[m] + NW * RPW - 1) / (NW * RPW);
+    hipLaunchKernelGGL((matvec_kernel<RPW, VEC>), dim3(blocks), dim3(NT), (size_t)a->K * sizeof(float), st, *a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
+    if (a->n_mat < 1 || a->n_mat > G3K_MATVEC_MAX || a->K < 1 || a->K > G3K_MATVEC_MAX_K || !a->x)
+        return (int)hipErrorInvalidValue;
+    bool vec = a->K % 8 == 0 && ((uintptr_t)a->x & 15) == 0;
+    long long rows = 0;
+    for (int m = 0; m < a->n_mat; m++) {
+        if (a->M[m] < 1 || !a->A[m] || !a->y[m]) return (int)hipErrorInvalidValue;
+        vec = vec && ((uintptr_t)a->A[m] & 15) == 0;
+        rows += a->M[m];
+    }
+    if (rows > (1LL << 30)) return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    // two rows per wave once there are enough rows to fill the chip with them
+    if (rows >= 16384) return (int)(vec ? launch<2, true>(a, st) : launch<2, false>(a, st));
+    return (int)(vec ? launch<1, true>(a, st) : launch<1, false>(a, st));
+}

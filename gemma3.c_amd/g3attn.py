@@ -93,10 +93,15 @@ def lib():
     L.g3attn_last_error.restype = C.c_char_p
     L.g3attn_profile_enable.argtypes = [_vp, C.c_int]
     L.g3attn_profile_read.argtypes = [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]
+    L.g3attn_matvec_bf16.argtypes = [_f32p, _vp, _f32p, C.c_int, C.c_int, _vp]
+    L.g3attn_matvec_bf16.restype = None
+    L.g3attn_matvec_bf16_device.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int]
+    L.g3attn_qkv_proj_device.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
                  "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
-                 "g3attn_profile_enable", "g3attn_profile_read"):
+                 "g3attn_profile_enable", "g3attn_profile_read", "g3attn_matvec_bf16_device",
+                 "g3attn_qkv_proj_device"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -146,6 +151,20 @@ def gqa(q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim=256, scale=0
     if err:
         raise G3AttnError(ERR_INVALID_ARG, err)
     return out
+
+
+def matvec_bf16(A, x) -> np.ndarray:
+    """gemma3_matvec_bf16-shaped call (gemma3_kernels.h:217-218) on the GPU:
+    A [M][K] bf16 bit patterns (uint16), x [K] fp32 -> y [M] fp32."""
+    A = np.ascontiguousarray(A, dtype=np.uint16)
+    M, K = A.shape
+    y = np.full(M, np.nan, dtype=np.float32)
+    lib().g3attn_matvec_bf16(y, A.ctypes.data_as(_vp), np.ascontiguousarray(x, dtype=np.float32),
+                             M, K, None)
+    err = last_error()
+    if err:
+        raise G3AttnError(ERR_INVALID_ARG, err)
+    return y
 
 
 class Context:
@@ -249,6 +268,12 @@ class Context:
     def prefill_device(self, layer, start_pos, n, Q, K, V, q_norm, k_norm, out):
         _check(lib().g3attn_prefill_device(self._h, layer, start_pos, n, Q, K, V, q_norm, k_norm,
                                            out))
+
+    def matvec_bf16_device(self, y, A, x, M, K):
+        _check(lib().g3attn_matvec_bf16_device(self._h, y, A, x, M, K))
+
+    def qkv_proj_device(self, x, wq, wk, wv, q, k, v):
+        _check(lib().g3attn_qkv_proj_device(self._h, x, wq, wk, wv, q, k, v))
 
     def kv_append(self, layer, start_pos, K, V, k_norm=None):
         K = np.ascontiguousarray(K, np.float32)

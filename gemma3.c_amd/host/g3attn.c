@@ -823,6 +823,70 @@ int g3attn_prefill(g3attn_ctx *c, int layer, int start_pos, int n, const float *
     return G3_OK;
 }
 
+/* ------------------------------------------------------------------ GEMV */
+
+static int matvec_check(int M, int K, const void *y, const void *A, const void *x, const char *who) {
+    if (!y || !A || !x || M < 1 || K < 1) {
+        set_err("%s: null buffer or M / K < 1", who);
+        return G3_ERR_INVALID_ARG;
+    }
+    if (K > G3K_MATVEC_MAX_K) {
+        set_err("%s: K = %d > %d", who, K, G3K_MATVEC_MAX_K);
+        return G3_ERR_INVALID_ARG;
+    }
+    return G3_OK;
+}
+
+int g3attn_matvec_bf16_device(g3attn_ctx *c, float *y, const uint16_t *A, const float *x, int M, int K) {
+    if (!c) {
+        set_err("g3attn_matvec_bf16_device: null context");
+        return G3_ERR_INVALID_ARG;
+    }
+    int rc = matvec_check(M, K, y, A, x, "g3attn_matvec_bf16_device");
+    if (rc) return rc;
+    hipSetDevice(c->device);
+    g3k_matvec_args a;
+    memset(&a, 0, sizeof a);
+    a.x = x;
+    a.K = K;
+    a.n_mat = 1;
+    a.A[0] = A;
+    a.y[0] = y;
+    a.M[0] = M;
+    rc = g3k_matvec(&a, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_matvec_bf16_device launch");
+    return G3_OK;
+}
+
+int g3attn_qkv_proj_device(g3attn_ctx *c, const float *x, const uint16_t *wq, const uint16_t *wk,
+                           const uint16_t *wv, float *q, float *k, float *v) {
+    if (!c || !x || !wq || !wk || !wv || !q || !k || !v) {
+        set_err("g3attn_qkv_proj_device: null context or buffer");
+        return G3_ERR_INVALID_ARG;
+    }
+    const int K = c->cfg.hidden_size;
+    int rc = matvec_check(1, K, q, wq, x, "g3attn_qkv_proj_device");
+    if (rc) return rc;
+    hipSetDevice(c->device);
+    g3k_matvec_args a;
+    memset(&a, 0, sizeof a);
+    a.x = x;
+    a.K = K;
+    a.n_mat = 3;
+    a.A[0] = wq;
+    a.y[0] = q;
+    a.M[0] = c->cfg.num_heads * D;
+    a.A[1] = wk;
+    a.y[1] = k;
+    a.M[1] = c->cfg.num_kv_heads * D;
+    a.A[2] = wv;
+    a.y[2] = v;
+    a.M[2] = c->cfg.num_kv_heads * D;
+    rc = g3k_matvec(&a, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_qkv_proj_device launch");
+    return G3_OK;
+}
+
 /* ------------------------------------------------------------------ gemma3_gqa */
 
 /* Process-wide state of the gemma3_gqa-shaped entry point. */
@@ -913,5 +977,56 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
     g_err[0] = 0;
     pthread_mutex_lock(&g_gqa.lock);
     gqa_run(output, q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim, scale, mask);
+    pthread_mutex_unlock(&g_gqa.lock);
+}
+
+/* Host-pointer GEMV through the same process-wide stream; its own grow-on-
+ * demand device buffer holds A, x and y. */
+static struct {
+    void *buf;
+    size_t cap;
+} g_mv = {NULL, 0};
+
+static int matvec_run(float *y, const uint16_t *A, const float *x, int M, int K) {
+    int rc = matvec_check(M, K, y, A, x, "g3attn_matvec_bf16");
+    if (rc) return rc;
+    rc = gqa_init();
+    if (rc) return rc;
+    hipSetDevice(g_gqa.device);
+    const size_t ab = align256((size_t)M * K * sizeof(uint16_t)), xb = align256((size_t)K * 4);
+    const size_t need = ab + xb + (size_t)M * 4;
+    if (need > g_mv.cap) {
+        hipFree(g_mv.buf);
+        g_mv.buf = NULL;
+        g_mv.cap = 0;
+        if (!alloc_dev(&g_mv.buf, need, "matvec buffers")) return G3_ERR_OUT_OF_MEMORY;
+        g_mv.cap = need;
+    }
+    unsigned char *b = (unsigned char *)g_mv.buf;
+    uint16_t *dA = (uint16_t *)b;
+    float *dx = (float *)(b + ab), *dy = (float *)(b + ab + xb);
+    hipStream_t s = g_gqa.stream;
+    HIP_TRY(hipMemcpyAsync(dA, A, (size_t)M * K * sizeof(uint16_t), hipMemcpyHostToDevice, s), "g3attn_matvec_bf16 upload");
+    HIP_TRY(hipMemcpyAsync(dx, x, (size_t)K * 4, hipMemcpyHostToDevice, s), "g3attn_matvec_bf16 upload");
+    g3k_matvec_args a;
+    memset(&a, 0, sizeof a);
+    a.x = dx;
+    a.K = K;
+    a.n_mat = 1;
+    a.A[0] = dA;
+    a.y[0] = dy;
+    a.M[0] = M;
+    rc = g3k_matvec(&a, s);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_matvec_bf16 launch");
+    HIP_TRY(hipMemcpyAsync(y, dy, (size_t)M * 4, hipMemcpyDeviceToHost, s), "g3attn_matvec_bf16 download");
+    HIP_TRY(hipStreamSynchronize(s), "g3attn_matvec_bf16");
+    return G3_OK;
+}
+
+void g3attn_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K, float *scratch) {
+    (void)scratch;
+    g_err[0] = 0;
+    pthread_mutex_lock(&g_gqa.lock);
+    matvec_run(y, A, x, M, K);
     pthread_mutex_unlock(&g_gqa.lock);
 }

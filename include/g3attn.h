@@ -144,6 +144,28 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
                 int n_heads, int n_kv_heads, int seq_len, int head_dim,
                 float scale, const float *mask, float *scores_buf);
 
+/* y [M] = A [M][K] . x [K] with A bf16 row-major and fp32 x, y: the same
+ * signature and arithmetic as gemma3_matvec_bf16 (gemma3_kernels.h:217-218,
+ * gemma3_kernels.c:188-238; fp32 accumulation, summation order differs).
+ * scratch is accepted and unused.  Host pointers: A is copied to the device
+ * on every call, so this form is for parity and drop-in use; weights that
+ * stay on the device go through g3attn_matvec_bf16_device.  Runs on the
+ * default device through a process-wide context; failures leave y untouched
+ * and set g3attn_last_error (the reference returns void). */
+void g3attn_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K, float *scratch);
+
+/* Device-pointer form of g3attn_matvec_bf16 on the context stream (replaces
+ * matvec_bf16_dispatch, gemma3_transformer.c:38-49, for resident weights).
+ * K <= 40960; A and x 16-byte aligned with K % 8 == 0 take the vector path. */
+int g3attn_matvec_bf16_device(g3attn_ctx *ctx, float *y, const uint16_t *A, const float *x, int M, int K);
+
+/* The Q, K and V projections of layer_attention (gemma3_transformer.c:290-292)
+ * in one launch: q [num_heads*head_dim] = wq . x, k / v [num_kv_heads*head_dim]
+ * = wk / wv . x, x [hidden_size]; weights bf16 [rows][hidden_size].  Device
+ * pointers, on the context stream; feeds g3attn_decode_device directly. */
+int g3attn_qkv_proj_device(g3attn_ctx *ctx, const float *x, const uint16_t *wq, const uint16_t *wk,
+                           const uint16_t *wv, float *q, float *k, float *v);
+
 /* The context's HIP stream (hipStream_t), for callers that interleave their
  * own work; and a wait for everything queued on it. */
 void *g3attn_stream(g3attn_ctx *ctx);

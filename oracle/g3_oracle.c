@@ -94,6 +94,36 @@ void g3o_rope_apply(float *x, const float *freqs, int head_dim, int pos) {
     }
 }
 
+/* gemma3_kernels.c:146-186 (avx2_bf16_dot) as called by gemma3_matvec_bf16
+ * (:188-238) in the reference's AVX2 build.  Lane j of accumulator 0 sums
+ * elements 16 b + j, lane j of accumulator 1 elements 16 b + 8 + j (fused
+ * multiply-add, one rounding each); a remaining block of 8 goes to
+ * accumulator 0.  The horizontal sum adds acc1 into acc0 lane-wise, then lanes
+ * l and l + 4, then l and l + 2, then lanes 0 and 1; the tail adds
+ * bf16(a) * x one element at a time. */
+static float matvec_row(const uint16_t *a, const float *x, int K) {
+    float acc0[8] = {0}, acc1[8] = {0};
+    int k = 0;
+    for (; k + 15 < K; k += 16)
+        for (int j = 0; j < 8; j++) {
+            acc0[j] = fmaf(g3o_bf16_to_f32(a[k + j]), x[k + j], acc0[j]);
+            acc1[j] = fmaf(g3o_bf16_to_f32(a[k + 8 + j]), x[k + 8 + j], acc1[j]);
+        }
+    for (; k + 7 < K; k += 8)
+        for (int j = 0; j < 8; j++) acc0[j] = fmaf(g3o_bf16_to_f32(a[k + j]), x[k + j], acc0[j]);
+    float s8[8], s4[4], s2[2];
+    for (int j = 0; j < 8; j++) s8[j] = acc0[j] + acc1[j];
+    for (int j = 0; j < 4; j++) s4[j] = s8[j] + s8[j + 4];
+    for (int j = 0; j < 2; j++) s2[j] = s4[j] + s4[j + 2];
+    float r = s2[0] + s2[1];
+    for (; k < K; k++) r += g3o_bf16_to_f32(a[k]) * x[k];
+    return r;
+}
+
+void g3o_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K) {
+    for (int i = 0; i < M; i++) y[i] = matvec_row(A + (size_t)i * K, x, K);
+}
+
 /* gemma3_kernels.c:396-415.  Max, exp(x - max) with running sum, scale by 1/sum. */
 void g3o_softmax(float *x, int n) {
     float m = x[0];

@@ -20,6 +20,7 @@
  *   g3o_prefill                              gemma3_transformer.c:641-692
  *   g3o_prefill_mt / g3o_prefill_rows        the same loop, tokens in parallel
  *   g3o_is_global_layer / g3o_layer_theta    gemma3.h:347-360
+ *   g3o_matvec_bf16                          gemma3_kernels.c:146-238 (AVX2 order)
  *
  * How each function is pinned (tests/test_oracle_*.py):
  *   - against golden vectors written by the real reference sources compiled
@@ -78,6 +79,13 @@ void g3o_gqa(float *out, const float *q, const float *k, const float *v,
 void g3o_gqa_rows(float *out, const float *q, const float *k, const float *v,
                   const int *rows, int n_heads, int n_kv_heads, int seq_len,
                   int head_dim, float scale, const float *mask, float *scores);
+
+/* gemma3_matvec_bf16: y [M] = A [M][K] (bf16 row-major) . x [K], fp32.  The
+ * sum follows the reference's AVX2 build (the path its `make fast` flags
+ * select): per row, two 8-lane fused multiply-add accumulators over blocks of
+ * 16 elements, one over a remaining block of 8, lane sums combined as
+ * (acc0 + acc1) -> halves -> pairs -> one, then a scalar tail. */
+void g3o_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K);
 
 /* cache_kv: copies k, v (kv_size floats each) into slot pos or pos % window. */
 void g3o_cache_kv(float *k_cache, float *v_cache, const float *k, const float *v,

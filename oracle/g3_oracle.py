@@ -106,6 +106,7 @@ def lib():
         L.g3o_norm_rope_batch.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_void_p, _f32p,
                                           C.c_int, C.c_float, C.c_int]
         L.g3o_gen_normal_bf16.argtypes = [_f32p, C.c_size_t, C.c_uint64, C.c_size_t, C.c_int]
+        L.g3o_matvec_bf16.argtypes = [_f32p, _u16p, _f32p, C.c_int, C.c_int]
         L.g3o_splitmix64.argtypes = [C.c_uint64, C.c_uint64]
         L.g3o_splitmix64.restype = C.c_uint64
         L.g3o_fnv1a64.argtypes = [C.c_void_p, C.c_size_t]
@@ -150,6 +151,11 @@ def ref():
                                       _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                       C.c_int, C.c_int]
         R.ref_time_decode.restype = C.c_double
+        R.ref_matvec_bf16.argtypes = [_f32p, _u16p, _f32p, C.c_int, C.c_int]
+        R.ref_layer_attention.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, _u16p, C.c_void_p,
+                                          C.c_void_p, _f32p, _f32p, _f32p, C.c_int, C.c_int,
+                                          C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        R.ref_layer_attention.restype = C.c_int
         _ref = R
     return _ref
 
@@ -224,6 +230,37 @@ def gqa(q, k, v, n_heads, n_kv, seq_len, d=256, scale=0.0625, mask=None, use_ref
     f(out, np.ascontiguousarray(q), np.ascontiguousarray(k), np.ascontiguousarray(v),
       n_heads, n_kv, seq_len, d, scale, _ptr(m), None)
     return out
+
+
+def matvec_bf16(A: np.ndarray, x: np.ndarray, use_ref=False) -> np.ndarray:
+    """gemma3_matvec_bf16 (gemma3_kernels.c:188-238): A [M][K] bf16 bits (uint16),
+    x [K] fp32 -> y [M] fp32, in the reference AVX2 build's summation order."""
+    A = np.ascontiguousarray(A, dtype=np.uint16)
+    M, K = A.shape
+    y = np.empty(M, dtype=np.float32)
+    (ref().ref_matvec_bf16 if use_ref else lib().g3o_matvec_bf16)(
+        y, A, np.ascontiguousarray(x, dtype=np.float32), M, K)
+    return y
+
+
+def layer_attention(cfg: Config, layer: int, pos: int, x, wq, wk, wv, wo, k_cache, v_cache,
+                    table, q_norm=None, k_norm=None, use_ref=False):
+    """The whole of layer_attention (gemma3_transformer.c:258-356) for one token:
+    x [hidden] -> Q/K/V GEMVs -> attention section -> o_proj GEMV -> [hidden].
+    The caches are updated in place."""
+    hidden = x.size
+    if use_ref:
+        out = np.empty(hidden, dtype=np.float32)
+        rc = ref().ref_layer_attention(out, np.ascontiguousarray(x, np.float32), wq, wk, wv, wo,
+                                       _ptr(q_norm), _ptr(k_norm), k_cache, v_cache, table,
+                                       cfg.num_heads, cfg.num_kv_heads, hidden, layer, pos,
+                                       cfg.max_context, cfg.sliding_window)
+        if rc:
+            raise RuntimeError(f"ref_layer_attention rc={rc}")
+        return out
+    q, k, v = matvec_bf16(wq, x), matvec_bf16(wk, x), matvec_bf16(wv, x)
+    attn, _, _ = layer_decode(cfg, layer, pos, q, k, v, k_cache, v_cache, table, q_norm, k_norm)
+    return matvec_bf16(wo, attn)
 
 
 def layer_decode(cfg: Config, layer: int, pos: int, q, k, v, k_cache, v_cache, table,

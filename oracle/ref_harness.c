@@ -77,6 +77,37 @@ void ref_gqa(float *out, const float *q, const float *k, const float *v, int hq,
     gemma3_gqa(out, q, k, v, hq, hkv, seq_len, d, scale, mask, scores);
 }
 int ref_is_global_layer(int l) { return gemma3_is_global_layer(l); }
+void ref_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K) {
+    gemma3_matvec_bf16(y, A, x, M, K, NULL);
+}
+
+/* The whole of layer_attention (gemma3_transformer.c:258-356) for one token
+ * with caller-given projection weights: x [hidden] -> out [hidden] through
+ * the Q/K/V GEMVs, QK-norm, RoPE, cache_kv, GQA and the o_proj GEMV. */
+int ref_layer_attention(float *out, const float *x, const uint16_t *wq, const uint16_t *wk,
+                        const uint16_t *wv, const uint16_t *wo, const uint16_t *q_norm,
+                        const uint16_t *k_norm, float *k_cache, float *v_cache, const float *rope,
+                        int hq, int hkv, int hidden, int layer, int pos, int max_context, int window) {
+    gemma3_config cfg = harness_cfg(hq, hkv, max_context, window);
+    cfg.hidden_size = hidden;
+    const int qs = hq * RH_D, ks = hkv * RH_D;
+    const int cap = max_context > window ? max_context : window;
+    float *qb = (float *)malloc((size_t)qs * 4), *kb = (float *)malloc((size_t)ks * 4);
+    float *vb = (float *)malloc((size_t)ks * 4), *ab = (float *)malloc((size_t)qs * 4);
+    float *mask = (float *)malloc((size_t)cap * 4), *scores = (float *)malloc((size_t)cap * 4);
+    float *tmp = (float *)malloc((size_t)(hidden > qs ? hidden : qs) * 4);
+    int rc = 0;
+    if (!qb || !kb || !vb || !ab || !mask || !scores || !tmp) { rc = -4; goto done; }
+    layer_kv_cache cache;
+    cache.k = k_cache;
+    cache.v = v_cache;
+    cache.pos = pos;
+    layer_attention(out, x, wq, wk, wv, wo, q_norm, k_norm, &cache, qb, kb, vb, ab,
+                    mask, scores, tmp, rope, NULL, &cfg, layer, pos);
+done:
+    free(qb); free(kb); free(vb); free(ab); free(mask); free(scores); free(tmp);
+    return rc;
+}
 
 /* One decode step through the reference's layer_attention.
  * q/k/v: pre-norm inputs (not modified).  k_cache/v_cache: the layer's cache,

@@ -10,6 +10,7 @@ generator drift on another machine is caught before outputs are compared.
 
     python tests/golden/make_golden.py            # all fixtures
     python tests/golden/make_golden.py --no-big   # skip the configs[3] run (~1-2 min)
+    python tests/golden/make_golden.py --only matvec
 
 Fixtures (numpy .npz, allow_pickle=False):
   rope.npz        RoPE table bits: full-table hashes + sampled rows
@@ -22,6 +23,10 @@ Fixtures (numpy .npz, allow_pickle=False):
                   small / chunked / ring-wrap cases, configs[2] and configs[3]:
                   sampled rows + (sum, sum of squares) of every row, and the
                   hashes of the final cache
+  matvec.npz      gemma3_matvec_bf16 (gemma3_kernels.c:188-238) at the Q / K /
+                  O projection shapes and ragged ones, and the whole of
+                  layer_attention (gemma3_transformer.c:258-356, x -> Q/K/V
+                  GEMVs -> attention -> o_proj) on seeded bf16 weights
 """
 from __future__ import annotations
 
@@ -176,14 +181,71 @@ def prefill_fixture(big: bool):
     return out
 
 
+def weights_bf16(M, K, seed):
+    """Seeded N(0,1) bf16 weights scaled by 2^-6 (exact in bf16), as uint16 bits."""
+    a = (O.gen_normal_bf16(M * K, seed) * np.float32(2.0 ** -6)).astype(np.float32)
+    return (a.view(np.uint32) >> 16).astype(np.uint16).reshape(M, K)
+
+
+MATVEC_SHAPES = {"q": (2048, 2560), "kv": (1024, 2560), "o": (2560, 2048),
+                 "r1": (37, 1000), "r2": (5, 2565), "r3": (1, 1)}
+
+
+def matvec_case(name):
+    M, K = MATVEC_SHAPES[name]
+    return weights_bf16(M, K, 0x9000 + M + 7 * K), O.gen_normal_bf16(K, 0x9800 + K)
+
+
+def layer_attention_case(layer, pos, hidden=2560):
+    """Inputs of one full layer_attention call: x, the four projection
+    matrices and a cache holding positions the layer keeps before pos."""
+    cfg = O.Config(max_context=8192)
+    wq, wk, wv = (weights_bf16(r, hidden, s) for r, s in ((2048, 0x9100), (1024, 0x9200), (1024, 0x9300)))
+    wo = weights_bf16(hidden, 2048, 0x9400)
+    x = O.gen_normal_bf16(hidden, 0x9500 + pos)
+    table = O.rope_table(8192, cfg.theta(layer), use_ref=True)
+    is_g = O.is_global_layer(layer)
+    lo = 0 if is_g else max(0, pos - cfg.sliding_window)
+    n = pos - lo
+    K = O.gen_normal_bf16(n * KS, 0x9600, lo * KS).reshape(n, KS)
+    V = O.gen_normal_bf16(n * KS, 0x9700, lo * KS).reshape(n, KS)
+    O.norm_rope_batch(K.reshape(n, 4, 256), table, lo, O.zero_norm())
+    rows = cfg.cache_rows(layer)
+    Kc = np.zeros((rows, KS), np.float32)
+    Vc = np.zeros((rows, KS), np.float32)
+    slots = np.arange(lo, pos) if is_g else np.arange(lo, pos) % cfg.sliding_window
+    Kc[slots], Vc[slots] = K, V
+    return cfg, table, x, wq, wk, wv, wo, Kc, Vc
+
+
+def matvec_fixture():
+    out = {}
+    for name in MATVEC_SHAPES:
+        A, x = matvec_case(name)
+        out[f"{name}_in_hash"] = np.array([h64(A), h64(x)], np.uint64)
+        out[f"{name}_y"] = O.matvec_bf16(A, x, use_ref=True)
+    for name, (layer, pos) in {"la_g": (5, 1000), "la_l": (0, 1500)}.items():
+        cfg, table, x, wq, wk, wv, wo, Kc, Vc = layer_attention_case(layer, pos)
+        out[f"{name}_meta"] = np.array([layer, pos], np.int32)
+        out[f"{name}_in_hash"] = np.array([h64(x), h64(wq), h64(wk), h64(wv), h64(wo), h64(Vc)], np.uint64)
+        zn = O.zero_norm()
+        out[f"{name}_y"] = O.layer_attention(cfg, layer, pos, x, wq, wk, wv, wo, Kc, Vc, table, zn, zn,
+                                             use_ref=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--no-big", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of fixtures to write (default: all)")
     args = ap.parse_args()
     if not O.have_ref():
         sys.exit("oracle/_ref/libg3ref.so is not built (needs /root/reference at build time)")
+    ap_only = set(filter(None, args.only.split(",")))
     for name, fn in (("rope", rope_fixture), ("kernels", kernels_fixture), ("decode", decode_fixture),
-                     ("prefill", lambda: prefill_fixture(not args.no_big))):
+                     ("prefill", lambda: prefill_fixture(not args.no_big)), ("matvec", matvec_fixture)):
+        if ap_only and name not in ap_only:
+            continue
         t0 = time.time()
         data = fn()
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **data)

@@ -40,6 +40,65 @@ def g3attn():
     return _g3
 
 
+class DeviceBuffer:
+    """Device memory for the _device entry points, allocated through the HIP
+    runtime the product library itself links (no torch in the test process,
+    so exactly one HIP runtime is loaded)."""
+
+    _hip = None
+
+    @classmethod
+    def hip(cls):
+        if cls._hip is None:
+            import ctypes as C
+            g3attn().lib()                     # the library's runtime is loaded first
+            h = C.CDLL("libamdhip64.so.7")
+            h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+            h.hipFree.argtypes = [C.c_void_p]
+            h.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+            h.hipDeviceSynchronize.argtypes = []
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self, nbytes: int):
+        import ctypes as C
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        rc = self.hip().hipMalloc(C.byref(p), max(self.nbytes, 1))
+        assert rc == 0, f"hipMalloc({self.nbytes}) -> {rc}"
+        self.ptr = int(p.value)
+
+    @classmethod
+    def of(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        assert self.hip().hipMemcpy(self.ptr + offset, a.ctypes.data, a.nbytes, 1) == 0
+
+    def download(self, dtype, shape, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        assert self.hip().hipDeviceSynchronize() == 0
+        assert self.hip().hipMemcpy(out.ctypes.data, self.ptr + offset, out.nbytes, 2) == 0
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.hip().hipFree(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
     """max |got - ref| / RMS(ref)."""
     ref = np.asarray(ref, dtype=np.float64)

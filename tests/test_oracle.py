@@ -389,3 +389,82 @@ def test_restatement_equals_reference_build_random():
         # reductions differently, so agreement is to fp32 rounding, not bits
         assert rel(a, b) < 1e-5
         assert rel(Kc1, Kc2) < 1e-6 and np.array_equal(Vc1, Vc2)
+
+
+# ---------------------------------------------------------------- GEMV (next row: the projections)
+
+def _mg():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("make_golden", os.path.join(GOLD, "make_golden.py"))
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m
+
+
+def _bf16_f64(A):
+    return (A.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _matvec_bound(A, x):
+    """fp32 accumulation error bound per row: K * 2^-24 * sum |a_k x_k|."""
+    K = A.shape[1]
+    return K * 2.0 ** -24 * (np.abs(_bf16_f64(A)) @ np.abs(x.astype(np.float64))) + 1e-30
+
+
+def test_matvec_closed_form_and_mutants():
+    """gemma3_matvec_bf16 against an fp64 dot product on every shape class
+    (vector blocks of 16, a block of 8, scalar tails); a transposed operand, a
+    truncated row or a dropped tail fails the same bound."""
+    rng = np.random.default_rng(7)
+    for M, K in ((3, 1), (2, 7), (4, 8), (5, 16), (3, 24), (6, 37), (9, 1000), (2, 2565)):
+        A = (rng.integers(0x3B00, 0x3F00, size=(M, K)) | (rng.integers(0, 2, size=(M, K)) << 15)).astype(np.uint16)
+        x = rng.standard_normal(K).astype(np.float32)
+        y = O.matvec_bf16(A, x)
+        y64 = _bf16_f64(A) @ x.astype(np.float64)
+        assert np.all(np.abs(y - y64) <= _matvec_bound(A, x)), (M, K)
+        if K > 1:
+            wrong_tail = _bf16_f64(A[:, :-1]) @ x[:-1].astype(np.float64)
+            assert np.any(np.abs(y - wrong_tail) > _matvec_bound(A, x)), (M, K)
+        if M == K or M > 1:
+            shuffled = _bf16_f64(A[::-1]) @ x.astype(np.float64)
+            assert np.any(np.abs(y - shuffled) > _matvec_bound(A, x)), (M, K)
+    A = (rng.integers(0x3B00, 0x3F00, size=(8, 8))).astype(np.uint16)
+    x = rng.standard_normal(8).astype(np.float32)
+    assert np.any(np.abs(O.matvec_bf16(A, x) - _bf16_f64(A.T) @ x) > _matvec_bound(A, x))
+
+
+def test_matvec_matches_reference_golden():
+    MG = _mg()
+    g = gold("matvec")
+    for name in MG.MATVEC_SHAPES:
+        A, x = MG.matvec_case(name)
+        assert [h64(A), h64(x)] == list(g[f"{name}_in_hash"])
+        y = O.matvec_bf16(A, x)
+        # the reference's fast build reassociates its lane sums; a few ulps of each row's sum
+        assert np.all(np.abs(y - g[f"{name}_y"]) <= 4 * _matvec_bound(A, x) / A.shape[1] * 16), name
+
+
+def test_layer_attention_matches_reference_golden():
+    """The whole of layer_attention (Q/K/V GEMVs, attention section, o_proj)."""
+    MG = _mg()
+    g = gold("matvec")
+    for name in ("la_g", "la_l"):
+        layer, pos = (int(v) for v in g[f"{name}_meta"])
+        cfg, table, x, wq, wk, wv, wo, Kc, Vc = MG.layer_attention_case(layer, pos)
+        hs = g[f"{name}_in_hash"]
+        assert [hs[0], hs[1], hs[2], hs[3], hs[4], hs[5]] == [h64(x), h64(wq), h64(wk), h64(wv), h64(wo), h64(Vc)]
+        zn = O.zero_norm()
+        y = O.layer_attention(cfg, layer, pos, x, wq, wk, wv, wo, Kc, Vc, O.rope_table(8192, cfg.theta(layer)), zn, zn)
+        assert rel(y, g[f"{name}_y"]) < 1e-5, name
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="oracle/_ref not built (no reference sources)")
+def test_matvec_restatement_equals_reference_build_random():
+    rng = np.random.default_rng(11)
+    for M, K in ((7, 2560), (5, 2048), (3, 10240), (4, 33)):
+        # random bf16 bit patterns: any sign and mantissa, exponents 2^-20 .. 2^12
+        A = ((rng.integers(0, 2, size=(M, K)) << 15) | (rng.integers(107, 140, size=(M, K)) << 7)
+             | rng.integers(0, 128, size=(M, K))).astype(np.uint16)
+        x = rng.standard_normal(K).astype(np.float32)
+        y, yr = O.matvec_bf16(A, x), O.matvec_bf16(A, x, use_ref=True)
+        assert np.all(np.abs(y - yr) <= 4 * _matvec_bound(A, x) / K * 16), (M, K)

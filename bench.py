@@ -263,8 +263,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of sections to run (decode8k = the headline, local512, 128k, "
-                         "stack, prefill, prefill_local_N2048_w1024, prefill_global_N8192); "
-                         "default: all")
+                         "stack, gemv, prefill, prefill_local_N2048_w1024, prefill_global_N8192, "
+                         "prefill_global_N8192_fp32_values); default: all")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device-to-device copies of this many MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -417,6 +417,74 @@ def main():
             }
             log(f"[bench] stack {name}: {extra[f'decode_stack34_L131072_{name}']}")
         ctx.close()
+
+    # ---------------- next row: the layer's Q/K/V and O projections (bf16 GEMV)
+    if not only or "gemv" in only:
+        ctx = B.context(8192)
+        torch = B.torch
+        hid = 2560
+        nl = 34   # distinct weights per layer: 34 x 31.5 MB rotate past the 256 MB LLC
+
+        def wbf16(r, c):
+            return B.randn_bf16(r, c).mul_(2.0 ** -6).to(torch.bfloat16).view(torch.int16)
+        Ws = [(wbf16(QS, hid), wbf16(KS, hid), wbf16(KS, hid), wbf16(hid, QS)) for _ in range(nl)]
+        xs = B.randn_bf16(hid)
+        qo, ko, vo = (torch.empty(n, device=B.dev) for n in (QS, KS, KS))
+        attn_in = B.randn_bf16(QS)
+        yo = torch.empty(hid, device=B.dev)
+        torch.cuda.synchronize()
+        gemv_bytes = 2 * hid * (QS + 2 * KS) + 2 * hid * QS
+
+        def proj_calls():
+            cl = []
+            for wq, wk, wv, wo in Ws:
+                def f(wq=wq, wk=wk, wv=wv, wo=wo):
+                    ctx.qkv_proj_device(xs.data_ptr(), wq.data_ptr(), wk.data_ptr(), wv.data_ptr(),
+                                        qo.data_ptr(), ko.data_ptr(), vo.data_ptr())
+                    ctx.matvec_bf16_device(yo.data_ptr(), wo.data_ptr(), attn_in.data_ptr(), hid, QS)
+                cl.append(f)
+            return cl
+        cl = proj_calls()
+        region, per_call, _ = B.time_calls(ctx, cl, 340, 34)
+        extra["gemv_qkv_o_projections"] = {
+            "config": "one layer's Q/K/V projections (one fused launch) + O projection, Gemma3-4B "
+                      "shapes (hidden 2560), bf16 weights, 34 distinct layers rotated (1.07 GB)",
+            "us_per_layer": round(region / 340 * 1e6, 2),
+            "call_us": round(per_call * 1e6, 2),
+            "bytes_per_layer": gemv_bytes,
+            "GB/s": round(gemv_bytes / (region / 340) / 1e9, 1),
+            "frac_of_hbm_peak": round(gemv_bytes / (region / 340) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"[bench] gemv: {extra['gemv_qkv_o_projections']}")
+        # the whole of layer_attention at configs[1]'s position: projections +
+        # attention over 8192 cached positions + o_proj, one entry point
+        glob = [5, 11, 17, 23, 29]
+        for l in glob:
+            B.fill_layer(ctx, l, 8191)
+        zn16 = torch.zeros(D, dtype=torch.int16, device=B.dev)
+        la_out = torch.empty(hid, device=B.dev)
+        torch.cuda.synchronize()
+        la_calls = []
+        for i, l in enumerate(glob):
+            wq, wk, wv, wo = Ws[i]
+
+            def f(l=l, wq=wq, wk=wk, wv=wv, wo=wo):
+                ctx.layer_attention_device(l, 8191, xs.data_ptr(), wq.data_ptr(), wk.data_ptr(),
+                                           wv.data_ptr(), wo.data_ptr(), zn16.data_ptr(),
+                                           zn16.data_ptr(), la_out.data_ptr())
+            la_calls.append(f)
+        region, per_call, _ = B.time_calls(ctx, la_calls, 200, 20)
+        la_bytes = gemv_bytes + decode_bytes(8192)
+        extra["layer_attention_L8192"] = {
+            "config": "the whole of layer_attention for one token at pos 8191 of a global layer: "
+                      "Q/K/V projections, attention over 8192 positions, o_proj (5 layers rotated)",
+            "us_per_layer": round(region / 200 * 1e6, 2),
+            "bytes_per_layer": la_bytes,
+            "GB/s": round(la_bytes / (region / 200) / 1e9, 1),
+        }
+        log(f"[bench] layer_attention 8K: {extra['layer_attention_L8192']}")
+        ctx.close()
+        del Ws
 
     # ---------------- prefill.  The configs' inputs are
     # bf16-valued; the fp32 line feeds values off the bf16 grid, which takes the

@@ -141,9 +141,8 @@ int g3k_prefill(const g3k_prefill_args *a, void *stream);
 
 /* bf16-weight GEMV, y[m] = A[m] . x for up to G3K_MATVEC_MAX matrices that
  * share x (one launch): A[m] [M[m]][K] bf16 row-major, x [K], y[m] [M[m]]
- * fp32.  K <= G3K_MATVEC_MAX_K (x is staged in LDS). */
+ * fp32. */
 #define G3K_MATVEC_MAX 3
-#define G3K_MATVEC_MAX_K 40960
 typedef struct {
     const float *x;
     int K;

@@ -11,10 +11,11 @@
 // At decode batch 1 the GEMV is HBM-bound: 2 bytes of A per multiply-add.
 // Workgroup = 4 waves; each wave owns RPW consecutive rows.  Lane l reads the
 // 16-byte chunks 8 l + 512 j of each row, so one wave load covers 1 KiB of a
-// row, contiguous, and all of a row's loads are issued before the FMAs that
-// use them.  x is staged once per workgroup in LDS.  Row sums reduce over the
-// wave with DPP and permlane swaps.  Rows whose length is not a multiple of 8
-// (or unaligned buffers) take a lane-strided scalar path.
+// row, contiguous, and all of a row's loads (rows up to 4096 elements; longer
+// rows in rounds of that size) are issued, with the x chunks they meet, before
+// the FMAs that use them.  x is small and read through the caches.  Row sums
+// reduce over the wave with DPP and permlane swaps.  Rows whose length is not
+// a multiple of 8 (or unaligned buffers) take a lane-strided scalar path.
 //
 // One launch can serve up to three matrices that share x (the Q, K and V
 // projections of one token): workgroups are dealt to the matrices in order of
@@ -60,17 +61,14 @@ __device__ __forceinline__ int pick(const g3k_matvec_args &a, int rows_per_wg, i
 
 template <int RPW, bool VEC>
 __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
-    extern __shared__ float xs[];
     const int K = a.K;
     int row0;
     const int m = pick(a, NW * RPW, row0);
     if (m < 0) return;   // uniform over the workgroup
-    for (int i = threadIdx.x; i < K; i += NT) xs[i] = a.x[i];
-    __syncthreads();
-
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int M = a.M[m];
     const uint16_t *A = a.A[m];
+    const float *x = a.x;
     const int r0 = row0 + wave * RPW;
     float acc[RPW];
 #pragma unroll
@@ -78,35 +76,34 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
 
     if (VEC) {
         // 16-byte chunks: chunk c covers elements 8c .. 8c + 7; lane l takes
-        // chunks l, l + 64, ...; four chunks per row are loaded ahead
+        // chunks l, l + 64, ...  All CH chunks of a round (a whole row of up
+        // to 4096 elements) are requested, with their x, before any FMA.
+        constexpr int CH = 8;
         const int nch = K >> 3;
-        constexpr int U = 4;
-        for (int c0 = lane; c0 < nch; c0 += 64 * U) {
-            uint4 w[RPW][U];
+        for (int c0 = lane; c0 < nch; c0 += 64 * CH) {
+            uint4 w[RPW][CH];
+            float4 xa[CH], xb[CH];
 #pragma unroll
-            for (int u = 0; u < U; u++) {
+            for (int u = 0; u < CH; u++) {
                 const int c = c0 + 64 * u;
+                const bool ok = c < nch;
 #pragma unroll
                 for (int r = 0; r < RPW; r++) {
                     const int row = r0 + r < M ? r0 + r : M - 1;
-                    w[r][u] = c < nch ? *reinterpret_cast<const uint4 *>(A + (size_t)row * K + 8 * c)
-                                      : make_uint4(0, 0, 0, 0);
+                    w[r][u] = ok ? *reinterpret_cast<const uint4 *>(A + (size_t)row * K + 8 * c)
+                                 : make_uint4(0, 0, 0, 0);
                 }
+                xa[u] = ok ? *reinterpret_cast<const float4 *>(x + 8 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xb[u] = ok ? *reinterpret_cast<const float4 *>(x + 8 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int c = c0 + 64 * u;
-                if (c < nch) {
-                    const float4 xa = *reinterpret_cast<const float4 *>(xs + 8 * c);
-                    const float4 xb = *reinterpret_cast<const float4 *>(xs + 8 * c + 4);
+            for (int u = 0; u < CH; u++)
 #pragma unroll
-                    for (int r = 0; r < RPW; r++) acc[r] += dot8(w[r][u], xa, xb);
-                }
-            }
+                for (int r = 0; r < RPW; r++) acc[r] += dot8(w[r][u], xa[u], xb[u]);
         }
     } else {
         for (int k = lane; k < K; k += 64) {
-            const float xv = xs[k];
+            const float xv = x[k];
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
                 const int row = r0 + r < M ? r0 + r : M - 1;
@@ -125,14 +122,14 @@ template <int RPW, bool VEC>
 hipError_t launch(const g3k_matvec_args *a, hipStream_t st) {
     int blocks = 0;
     for (int m = 0; m < a->n_mat; m++) blocks += (a->M[m] + NW * RPW - 1) / (NW * RPW);
-    hipLaunchKernelGGL((matvec_kernel<RPW, VEC>), dim3(blocks), dim3(NT), (size_t)a->K * sizeof(float), st, *a);
+    hipLaunchKernelGGL((matvec_kernel<RPW, VEC>), dim3(blocks), dim3(NT), 0, st, *a);
     return hipGetLastError();
 }
 
 }  // namespace
 
 extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
-    if (a->n_mat < 1 || a->n_mat > G3K_MATVEC_MAX || a->K < 1 || a->K > G3K_MATVEC_MAX_K || !a->x)
+    if (a->n_mat < 1 || a->n_mat > G3K_MATVEC_MAX || a->K < 1 || !a->x)
         return (int)hipErrorInvalidValue;
     bool vec = a->K % 8 == 0 && ((uintptr_t)a->x & 15) == 0;
     long long rows = 0;

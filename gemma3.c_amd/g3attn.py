@@ -97,11 +97,13 @@ def lib():
     L.g3attn_matvec_bf16.restype = None
     L.g3attn_matvec_bf16_device.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int]
     L.g3attn_qkv_proj_device.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    L.g3attn_layer_attention_device.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
+                                                _vp, _vp, _vp]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
                  "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
                  "g3attn_profile_enable", "g3attn_profile_read", "g3attn_matvec_bf16_device",
-                 "g3attn_qkv_proj_device"):
+                 "g3attn_qkv_proj_device", "g3attn_layer_attention_device"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -274,6 +276,10 @@ class Context:
 
     def qkv_proj_device(self, x, wq, wk, wv, q, k, v):
         _check(lib().g3attn_qkv_proj_device(self._h, x, wq, wk, wv, q, k, v))
+
+    def layer_attention_device(self, layer, pos, x, wq, wk, wv, wo, q_norm, k_norm, out):
+        _check(lib().g3attn_layer_attention_device(self._h, layer, pos, x, wq, wk, wv, wo, q_norm,
+                                                   k_norm, out))
 
     def kv_append(self, layer, start_pos, K, V, k_norm=None):
         K = np.ascontiguousarray(K, np.float32)

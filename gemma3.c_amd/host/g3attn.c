@@ -108,6 +108,9 @@ struct g3attn_ctx {
     /* grow-on-demand prefill workspace (staged keys and values) */
     void *d_pf;
     size_t d_pf_cap;
+    /* layer_attention scratch: q | k | v | attn of one token */
+    float *d_la;
+    size_t d_la_cap;
     /* prefill: staging sets *d_vflag = pf_epoch when a value is not exactly
      * bf16 (the attention kernel then adds its V_lo pass) */
     int *d_vflag;
@@ -157,6 +160,7 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_big);
     hipFree(c->d_pf);
     hipFree(c->d_vflag);
+    hipFree(c->d_la);
     if (c->h_in) hipHostFree(c->h_in);
     if (c->h_out) hipHostFree(c->h_out);
     if (c->stream) hipStreamDestroy(c->stream);
@@ -825,13 +829,20 @@ int g3attn_prefill(g3attn_ctx *c, int layer, int start_pos, int n, const float *
 
 /* ------------------------------------------------------------------ GEMV */
 
+static int grow_la(g3attn_ctx *c, size_t bytes) {
+    if (bytes <= c->d_la_cap) return G3_OK;
+    HIP_TRY(hipStreamSynchronize(c->stream), "grow layer scratch");
+    hipFree(c->d_la);
+    c->d_la = NULL;
+    c->d_la_cap = 0;
+    if (!alloc_dev((void **)&c->d_la, bytes, "layer scratch")) return G3_ERR_OUT_OF_MEMORY;
+    c->d_la_cap = bytes;
+    return G3_OK;
+}
+
 static int matvec_check(int M, int K, const void *y, const void *A, const void *x, const char *who) {
     if (!y || !A || !x || M < 1 || K < 1) {
         set_err("%s: null buffer or M / K < 1", who);
-        return G3_ERR_INVALID_ARG;
-    }
-    if (K > G3K_MATVEC_MAX_K) {
-        set_err("%s: K = %d > %d", who, K, G3K_MATVEC_MAX_K);
         return G3_ERR_INVALID_ARG;
     }
     return G3_OK;
@@ -885,6 +896,27 @@ int g3attn_qkv_proj_device(g3attn_ctx *c, const float *x, const uint16_t *wq, co
     rc = g3k_matvec(&a, c->stream);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_qkv_proj_device launch");
     return G3_OK;
+}
+
+/* The whole of layer_attention for one token: Q/K/V GEMVs, the attention
+ * section (QK-norm, RoPE, cache write, GQA) and the o_proj GEMV. */
+int g3attn_layer_attention_device(g3attn_ctx *c, int layer, int pos, const float *x,
+                                  const uint16_t *wq, const uint16_t *wk, const uint16_t *wv,
+                                  const uint16_t *wo, const uint16_t *q_norm, const uint16_t *k_norm,
+                                  float *out) {
+    if (!c || !out) {
+        set_err("g3attn_layer_attention_device: null context or buffer");
+        return G3_ERR_INVALID_ARG;
+    }
+    const int qs = c->cfg.num_heads * D, ks = c->cfg.num_kv_heads * D;
+    int rc = grow_la(c, (size_t)(2 * qs + 2 * ks) * sizeof(float));
+    if (rc) return rc;
+    float *q = c->d_la, *k = q + qs, *v = k + ks, *attn = v + ks;
+    rc = g3attn_qkv_proj_device(c, x, wq, wk, wv, q, k, v);
+    if (rc) return rc;
+    rc = g3attn_decode_device(c, layer, pos, q, k, v, q_norm, k_norm, attn);
+    if (rc) return rc;
+    return g3attn_matvec_bf16_device(c, out, wo, attn, c->cfg.hidden_size, qs);
 }
 
 /* ------------------------------------------------------------------ gemma3_gqa */

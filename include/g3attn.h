@@ -156,7 +156,7 @@ void g3attn_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int 
 
 /* Device-pointer form of g3attn_matvec_bf16 on the context stream (replaces
  * matvec_bf16_dispatch, gemma3_transformer.c:38-49, for resident weights).
- * K <= 40960; A and x 16-byte aligned with K % 8 == 0 take the vector path. */
+ * A and x 16-byte aligned with K % 8 == 0 take the vector path. */
 int g3attn_matvec_bf16_device(g3attn_ctx *ctx, float *y, const uint16_t *A, const float *x, int M, int K);
 
 /* The Q, K and V projections of layer_attention (gemma3_transformer.c:290-292)
@@ -165,6 +165,17 @@ int g3attn_matvec_bf16_device(g3attn_ctx *ctx, float *y, const uint16_t *A, cons
  * pointers, on the context stream; feeds g3attn_decode_device directly. */
 int g3attn_qkv_proj_device(g3attn_ctx *ctx, const float *x, const uint16_t *wq, const uint16_t *wk,
                            const uint16_t *wv, float *q, float *k, float *v);
+
+/* The whole of layer_attention (gemma3_transformer.c:258-356) for one token
+ * at pos: x [hidden_size] -> Q/K/V projections -> QK-norm, RoPE, cache write,
+ * GQA -> o_proj -> out [hidden_size].  Weights bf16 (wq [num_heads*head_dim]
+ * [hidden], wk / wv [num_kv_heads*head_dim][hidden], wo [hidden]
+ * [num_heads*head_dim]), q_norm / k_norm as in g3attn_decode.  Device
+ * pointers, on the context stream (four launches, no host round trip). */
+int g3attn_layer_attention_device(g3attn_ctx *ctx, int layer, int pos, const float *x,
+                                  const uint16_t *wq, const uint16_t *wk, const uint16_t *wv,
+                                  const uint16_t *wo, const uint16_t *q_norm, const uint16_t *k_norm,
+                                  float *out);
 
 /* The context's HIP stream (hipStream_t), for callers that interleave their
  * own work; and a wait for everything queued on it. */

@@ -116,11 +116,34 @@ def test_layer_attention_on_gpu_matches_reference_golden(name):
     assert err < 1e-4
 
 
+def test_layer_attention_single_entry_point():
+    """g3attn_layer_attention_device (the four launches in one call) equals
+    the three-call chain above, bit for bit, and the reference's output."""
+    g = np.load(os.path.join(GOLD, "matvec.npz"), allow_pickle=False)
+    layer, pos = (int(v) for v in g["la_g_meta"])
+    cfg, table, x, wq, wk, wv, wo, Kc, Vc = MG.layer_attention_case(layer, pos)
+    with G.Context(G.default_config(max_context=8192), 8192,
+                   O.rope_table(8192, 10000.0), O.rope_table(8192, 1e6)) as ctx:
+        ctx.kv_write(layer, 0, Kc, Vc)
+        dx, dwq, dwk, dwv, dwo = (DeviceBuffer.of(a) for a in (x, wq, wk, wv, wo))
+        zn = DeviceBuffer.of(np.zeros(256, np.uint16))
+        out = DeviceBuffer(x.size * 4)
+        ctx.layer_attention_device(layer, pos, dx.ptr, dwq.ptr, dwk.ptr, dwv.ptr, dwo.ptr, zn.ptr,
+                                   zn.ptr, out.ptr)
+        got = out.download(np.float32, x.size)
+    err = rel_err(got, g["la_g_y"])
+    print(f"[layer_attention entry] rel_err={err:.3e}", flush=True)
+    assert err < 1e-4
+
+
 def test_matvec_errors():
     A = np.zeros((2, 8), np.uint16)
     with pytest.raises(G.G3AttnError):
         G.matvec_bf16(A[:0], np.zeros(8, np.float32))
-    big = np.zeros((1, 40968), np.uint16)
     with pytest.raises(G.G3AttnError):
-        G.matvec_bf16(big, np.zeros(40968, np.float32))
+        G.matvec_bf16(np.zeros((3, 0), np.uint16), np.zeros(0, np.float32))
     assert np.array_equal(G.matvec_bf16(A, np.ones(8, np.float32)), np.zeros(2, np.float32))
+    # long rows take several load rounds
+    A = MG.weights_bf16(3, 40968, 0xC100)
+    x = O.gen_normal_bf16(40968, 0xC200)
+    _check(G.matvec_bf16(A, x), O.matvec_bf16(A, x).astype(np.float64), A, x, "3x40968")

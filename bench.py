@@ -263,7 +263,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of sections to run (decode8k = the headline, local512, 128k, "
-                         "stack, gemv, prefill, prefill_local_N2048_w1024, prefill_global_N8192, "
+                         "stack, gemv, forward, prefill, prefill_local_N2048_w1024, prefill_global_N8192, "
                          "prefill_global_N8192_fp32_values); default: all")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device-to-device copies of this many MiB (the "
@@ -485,6 +485,68 @@ def main():
         log(f"[bench] layer_attention 8K: {extra['layer_attention_L8192']}")
         ctx.close()
         del Ws
+
+    # ---------------- next row: one token through the whole model (34 layers,
+    # tied logits) at configs[1]'s position, Gemma3-4B shapes, random weights
+    if not only or "forward" in only:
+        torch = B.torch
+        ctx = B.context(8192)
+        # every buffer is sized from the context's own config: the library reads
+        # vocab_size rows of the embedding for the logits and writes vocab_size floats
+        cfg = ctx.cfg
+        hid, inter, vocab, nl = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers
+        assert (hid, inter, vocab, nl) == (2560, 10240, 262208, 34)
+
+        def wbf16(r, c):
+            return B.randn_bf16(r, c).mul_(2.0 ** -6).to(torch.bfloat16).view(torch.int16)
+
+        def nbf16(n):
+            return B.randn_bf16(n).mul_(0.125).to(torch.bfloat16).view(torch.int16)
+        keep = []
+        W = G.Weights()
+
+        def dev(t):
+            keep.append(t)
+            return t.data_ptr()
+        W.embed_tokens, W.norm = dev(wbf16(vocab, hid)), dev(nbf16(hid))
+        for l in range(nl):
+            lw = W.layers[l]
+            lw.input_layernorm, lw.q_norm, lw.k_norm = dev(nbf16(hid)), dev(nbf16(D)), dev(nbf16(D))
+            lw.q_proj, lw.k_proj, lw.v_proj = dev(wbf16(QS, hid)), dev(wbf16(KS, hid)), dev(wbf16(KS, hid))
+            lw.o_proj = dev(wbf16(hid, QS))
+            lw.gate_proj, lw.up_proj = dev(wbf16(inter, hid)), dev(wbf16(inter, hid))
+            lw.down_proj = dev(wbf16(hid, inter))
+            lw.post_attention_layernorm = dev(nbf16(hid))
+            lw.pre_feedforward_layernorm = dev(nbf16(hid))
+            lw.post_feedforward_layernorm = dev(nbf16(hid))
+        logits = torch.empty(vocab, device=B.dev)
+        assert keep[0].numel() == vocab * hid and logits.numel() == vocab
+        torch.cuda.synchronize()
+        pos = 8191
+        layer_w = 2 * hid * (QS + 2 * KS) + 2 * hid * QS + 3 * 2 * hid * inter
+        n_glob = sum(1 for l in range(nl) if G.is_global_layer(l))
+        fwd_bytes = (nl * layer_w + 2 * vocab * hid + n_glob * decode_bytes(pos + 1)
+                     + (nl - n_glob) * decode_bytes(1024))
+
+        def fwd():
+            ctx.forward_device(W, 2, pos, logits.data_ptr(), True)
+        steps = 40
+        region, per_call, _ = B.time_calls(ctx, [fwd], steps, 5)
+        assert bool(torch.isfinite(logits).all())
+        t = region / steps
+        extra["forward_token_pos8191"] = {
+            "config": "one token through all 34 layers + final norm + tied logits at pos 8191 "
+                      "(g3attn_forward_device), Gemma3-4B shapes (hidden 2560, intermediate 10240, "
+                      "vocab 262208), random bf16 weights (7.8 GB), cache rows before pos zero",
+            "ms_per_token": round(t * 1e3, 3),
+            "tokens_per_s": round(1.0 / t, 1),
+            "bytes_per_token": fwd_bytes,
+            "GB/s": round(fwd_bytes / t / 1e9, 1),
+            "frac_of_hbm_peak": round(fwd_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        log(f"[bench] forward: {extra['forward_token_pos8191']}")
+        ctx.close()
+        del keep, W
 
     # ---------------- prefill.  The configs' inputs are
     # bf16-valued; the fp32 line feeds values off the bf16 grid, which takes the

@@ -150,9 +150,32 @@ typedef struct {
     const uint16_t *A[G3K_MATVEC_MAX];
     float *y[G3K_MATVEC_MAX];
     int M[G3K_MATVEC_MAX];
+    /* 0: y[m] = A[m] . x.  G3K_MV_GEGLU: n_mat = 2, M[0] == M[1],
+     * y[0] = gelu_tanh(A[0] . x) * (A[1] . x)  (gemma3_transformer.c:380-386) */
+    int mode;
 } g3k_matvec_args;
+#define G3K_MV_GEGLU 1
 
 int g3k_matvec(const g3k_matvec_args *a, void *stream);
+
+/* One-workgroup steps of a token's forward pass on a hidden vector of n
+ * floats (n <= G3K_LAYER_MAX_HIDDEN):
+ *   G3K_OP_EMBED:    x = bf16(embed[token][.]) * sqrt(n)
+ *   G3K_OP_NORM:     y = rmsnorm(x, w_next)
+ *   G3K_OP_RESIDUAL: t = rmsnorm(t, w_post) if w_post; x += t;
+ *                    then, if y: y = rmsnorm(x, w_next), or a copy of x if
+ *                    w_next is NULL
+ * rmsnorm(v, w) = v / sqrt(mean(v^2) + eps) * (1 + bf16(w)). */
+#define G3K_LAYER_MAX_HIDDEN 8192
+enum { G3K_OP_EMBED = 0, G3K_OP_NORM = 1, G3K_OP_RESIDUAL = 2 };
+typedef struct {
+    int op, n, token;
+    float eps;
+    const uint16_t *embed, *w_post, *w_next;
+    float *x, *t, *y;
+} g3k_layer_args;
+
+int g3k_layer_step(const g3k_layer_args *a, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,138 @@
+// layer.hip - the small kernels between the GEMVs of one token's forward pass
+// (gemma3_transformer_forward, gemma3_transformer.c:396-512): the embedding
+// row, the hidden-size RMSNorms with their residual adds.
+//
+// Each works on one hidden vector (a few thousand floats), so each is one
+// workgroup: latency, not bandwidth, is what they cost, and folding the
+// norms and adds that sit between two GEMVs into one launch is what matters.
+//   embed:     x = bf16(E[token]) * sqrt(hidden)          (:415-422)
+//   norm:      y = rmsnorm(x, w)                           (:444-446, 508)
+//   residual:  t = rmsnorm(t, w_post)  (if w_post)         (:463-466, 490-493)
+//              x = x + t                                   (:469, 496)
+//              y = rmsnorm(x, w_next)  (if y; a copy of x if w_next is NULL)
+// rmsnorm is gemma3_rmsnorm_bf16 (gemma3_kernels.c:289-304): mean of squares
+// + eps, 1 / sqrtf, then x * r * (1 + bf16(w)); the sum of squares is a tree
+// here instead of the reference's sequential loop.
+#include <hip/hip_runtime.h>
+
+#include "g3k.h"
+#include "g3k_device.h"
+
+namespace {
+
+using namespace g3k;
+
+constexpr int NT = 1024;
+constexpr int NW = NT / 64;
+constexpr int PER = 8;   // values per thread: hidden <= NT * PER
+
+// Sum over the workgroup; every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();   // red may still be read by an earlier call
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) s += red[w];
+    return s;
+}
+
+// r = 1 / sqrtf(mean(v^2) + eps) over the n values held PER per thread.
+__device__ __forceinline__ float rms_scale(const float (&v)[PER], int n, float eps, float *red) {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < PER; u++) ss += v[u] * v[u];
+    ss = block_sum(ss, red);
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+__global__ __launch_bounds__(NT) void embed_kernel(g3k_layer_args a) {
+    const int n = a.n;
+    const float scale = sqrtf((float)n);
+    const uint16_t *row = a.embed + (size_t)a.token * n;
+    for (int i = threadIdx.x; i < n; i += NT) a.x[i] = bf16f(row[i]) * scale;
+}
+
+__global__ __launch_bounds__(NT) void norm_kernel(g3k_layer_args a) {
+    __shared__ float red[NW];
+    const int n = a.n;
+    float v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + NT * u;
+        v[u] = i < n ? a.x[i] : 0.f;
+    }
+    const float r = rms_scale(v, n, a.eps, red);
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + NT * u;
+        if (i < n) a.y[i] = v[u] * r * (1.0f + bf16f(a.w_next[i]));
+    }
+}
+
+__global__ __launch_bounds__(NT) void residual_kernel(g3k_layer_args a) {
+    __shared__ float red[NW];
+    const int n = a.n;
+    float t[PER], x[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + NT * u;
+        t[u] = i < n ? a.t[i] : 0.f;
+        x[u] = i < n ? a.x[i] : 0.f;
+    }
+    if (a.w_post) {
+        const float r = rms_scale(t, n, a.eps, red);
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = threadIdx.x + NT * u;
+            t[u] = i < n ? t[u] * r * (1.0f + bf16f(a.w_post[i])) : 0.f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + NT * u;
+        x[u] = x[u] + t[u];
+        if (i < n) a.x[i] = x[u];
+    }
+    if (!a.y) return;   // uniform
+    if (a.w_next) {
+        const float r = rms_scale(x, n, a.eps, red);
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = threadIdx.x + NT * u;
+            if (i < n) a.y[i] = x[u] * r * (1.0f + bf16f(a.w_next[i]));
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = threadIdx.x + NT * u;
+            if (i < n) a.y[i] = x[u];
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int g3k_layer_step(const g3k_layer_args *a, void *stream) {
+    if (a->n < 1 || a->n > G3K_LAYER_MAX_HIDDEN) return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    switch (a->op) {
+        case G3K_OP_EMBED:
+            if (!a->embed || !a->x || a->token < 0) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(NT), 0, st, *a);
+            break;
+        case G3K_OP_NORM:
+            if (!a->x || !a->y || !a->w_next) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL(norm_kernel, dim3(1), dim3(NT), 0, st, *a);
+            break;
+        case G3K_OP_RESIDUAL:
+            if (!a->x || !a->t) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL(residual_kernel, dim3(1), dim3(NT), 0, st, *a);
+            break;
+        default:
+            return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}

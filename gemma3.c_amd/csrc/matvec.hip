@@ -19,7 +19,8 @@
 //
 // One launch can serve up to three matrices that share x (the Q, K and V
 // projections of one token): workgroups are dealt to the matrices in order of
-// their row blocks.
+// their row blocks.  The GEGLU mode computes the gate and up rows of the MLP
+// together and writes gelu_tanh(gate) * up (gemma3_transformer.c:380-386).
 #include <hip/hip_runtime.h>
 
 #include "g3k.h"
@@ -47,7 +48,8 @@ __device__ __forceinline__ float dot8(uint4 w, float4 xa, float4 xb) {
 // Matrix m of the launch and the workgroup's first row in it.
 __device__ __forceinline__ int pick(const g3k_matvec_args &a, int rows_per_wg, int &row0) {
     int b = blockIdx.x;
-    for (int m = 0; m < a.n_mat; m++) {
+    const int nm = a.mode == G3K_MV_GEGLU ? 1 : a.n_mat;
+    for (int m = 0; m < nm; m++) {
         const int nb = (a.M[m] + rows_per_wg - 1) / rows_per_wg;
         if (b < nb) {
             row0 = b * rows_per_wg;
@@ -59,70 +61,85 @@ __device__ __forceinline__ int pick(const g3k_matvec_args &a, int rows_per_wg, i
     return -1;
 }
 
-template <int RPW, bool VEC>
+// gelu with the tanh approximation, as gemma3_gelu_tanh_inplace
+// (gemma3_kernels.c:348-357): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float inner = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// NA dot products per wave: RPW consecutive rows of one matrix, or (GEGLU)
+// the same row of the gate and up matrices.
+template <int RPW, bool VEC, bool GEGLU>
 __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
+    constexpr int NA = GEGLU ? 2 : RPW;
     const int K = a.K;
     int row0;
     const int m = pick(a, NW * RPW, row0);
     if (m < 0) return;   // uniform over the workgroup
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int M = a.M[m];
-    const uint16_t *A = a.A[m];
     const float *x = a.x;
     const int r0 = row0 + wave * RPW;
-    float acc[RPW];
+    const uint16_t *rows[NA];
 #pragma unroll
-    for (int r = 0; r < RPW; r++) acc[r] = 0.f;
+    for (int j = 0; j < NA; j++) {
+        const int row = GEGLU ? (r0 < M ? r0 : M - 1) : (r0 + j < M ? r0 + j : M - 1);
+        rows[j] = a.A[GEGLU ? j : m] + (size_t)row * K;
+    }
+    float acc[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) acc[j] = 0.f;
 
     if (VEC) {
         // 16-byte chunks: chunk c covers elements 8c .. 8c + 7; lane l takes
         // chunks l, l + 64, ...  All CH chunks of a round (a whole row of up
         // to 4096 elements) are requested, with their x, before any FMA.
-        constexpr int CH = 8;
+        constexpr int CH = GEGLU ? 4 : 8;
         const int nch = K >> 3;
         for (int c0 = lane; c0 < nch; c0 += 64 * CH) {
-            uint4 w[RPW][CH];
+            uint4 w[NA][CH];
             float4 xa[CH], xb[CH];
 #pragma unroll
             for (int u = 0; u < CH; u++) {
                 const int c = c0 + 64 * u;
                 const bool ok = c < nch;
 #pragma unroll
-                for (int r = 0; r < RPW; r++) {
-                    const int row = r0 + r < M ? r0 + r : M - 1;
-                    w[r][u] = ok ? *reinterpret_cast<const uint4 *>(A + (size_t)row * K + 8 * c)
-                                 : make_uint4(0, 0, 0, 0);
-                }
+                for (int j = 0; j < NA; j++)
+                    w[j][u] = ok ? *reinterpret_cast<const uint4 *>(rows[j] + 8 * c) : make_uint4(0, 0, 0, 0);
                 xa[u] = ok ? *reinterpret_cast<const float4 *>(x + 8 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
                 xb[u] = ok ? *reinterpret_cast<const float4 *>(x + 8 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int u = 0; u < CH; u++)
 #pragma unroll
-                for (int r = 0; r < RPW; r++) acc[r] += dot8(w[r][u], xa[u], xb[u]);
+                for (int j = 0; j < NA; j++) acc[j] += dot8(w[j][u], xa[u], xb[u]);
         }
     } else {
         for (int k = lane; k < K; k += 64) {
             const float xv = x[k];
 #pragma unroll
-            for (int r = 0; r < RPW; r++) {
-                const int row = r0 + r < M ? r0 + r : M - 1;
-                acc[r] = fmaf(bf16f(A[(size_t)row * K + k]), xv, acc[r]);
-            }
+            for (int j = 0; j < NA; j++) acc[j] = fmaf(bf16f(rows[j][k]), xv, acc[j]);
         }
     }
+    if (GEGLU) {
+        const float g = wave_sum(acc[0]), u = wave_sum(acc[1]);
+        if (lane == 0 && r0 < M) a.y[0][r0] = gelu_tanh(g) * u;
+    } else {
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const float s = wave_sum(acc[r]);
-        if (lane == 0 && r0 + r < M) a.y[m][r0 + r] = s;
+        for (int j = 0; j < NA; j++) {
+            const float s = wave_sum(acc[j]);
+            if (lane == 0 && r0 + j < M) a.y[m][r0 + j] = s;
+        }
     }
 }
 
-template <int RPW, bool VEC>
+template <int RPW, bool VEC, bool GEGLU = false>
 hipError_t launch(const g3k_matvec_args *a, hipStream_t st) {
     int blocks = 0;
-    for (int m = 0; m < a->n_mat; m++) blocks += (a->M[m] + NW * RPW - 1) / (NW * RPW);
-    hipLaunchKernelGGL((matvec_kernel<RPW, VEC>), dim3(blocks), dim3(NT), 0, st, *a);
+    const int nm = GEGLU ? 1 : a->n_mat;
+    for (int m = 0; m < nm; m++) blocks += (a->M[m] + NW * RPW - 1) / (NW * RPW);
+    hipLaunchKernelGGL((matvec_kernel<RPW, VEC, GEGLU>), dim3(blocks), dim3(NT), 0, st, *a);
     return hipGetLastError();
 }
 
@@ -134,12 +151,19 @@ extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
     bool vec = a->K % 8 == 0 && ((uintptr_t)a->x & 15) == 0;
     long long rows = 0;
     for (int m = 0; m < a->n_mat; m++) {
-        if (a->M[m] < 1 || !a->A[m] || !a->y[m]) return (int)hipErrorInvalidValue;
+        // GEGLU writes one output (y[0]) from the two matrices
+        if (a->M[m] < 1 || !a->A[m] || (!a->y[m] && (a->mode != G3K_MV_GEGLU || m == 0)))
+            return (int)hipErrorInvalidValue;
         vec = vec && ((uintptr_t)a->A[m] & 15) == 0;
         rows += a->M[m];
     }
     if (rows > (1LL << 30)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
+    if (a->mode == G3K_MV_GEGLU) {
+        if (a->n_mat != 2 || a->M[0] != a->M[1]) return (int)hipErrorInvalidValue;
+        return (int)(vec ? launch<1, true, true>(a, st) : launch<1, false, true>(a, st));
+    }
+    if (a->mode != 0) return (int)hipErrorInvalidValue;
     // two rows per wave once there are enough rows to fill the chip with them
     if (rows >= 16384) return (int)(vec ? launch<2, true>(a, st) : launch<2, false>(a, st));
     return (int)(vec ? launch<1, true>(a, st) : launch<1, false>(a, st));

@@ -99,11 +99,13 @@ def lib():
     L.g3attn_qkv_proj_device.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     L.g3attn_layer_attention_device.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                                 _vp, _vp, _vp]
+    L.g3attn_forward_device.argtypes = [_vp, C.c_void_p, C.c_int, C.c_int, _vp, C.c_int, _vp]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
                  "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
                  "g3attn_profile_enable", "g3attn_profile_read", "g3attn_matvec_bf16_device",
-                 "g3attn_qkv_proj_device", "g3attn_layer_attention_device"):
+                 "g3attn_qkv_proj_device", "g3attn_layer_attention_device",
+                 "g3attn_forward_device"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -167,6 +169,23 @@ def matvec_bf16(A, x) -> np.ndarray:
     if err:
         raise G3AttnError(ERR_INVALID_ARG, err)
     return y
+
+
+class LayerWeights(C.Structure):
+    """g3attn_layer_weights: device addresses of one layer's bf16 tensors."""
+    _fields_ = [(n, C.c_void_p) for n in (
+        "input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
+        "post_attention_layernorm", "gate_proj", "up_proj", "down_proj",
+        "pre_feedforward_layernorm", "post_feedforward_layernorm")]
+
+
+MAX_LAYERS = 34
+
+
+class Weights(C.Structure):
+    """g3attn_weights (the layout of the reference's gemma3_weights_t)."""
+    _fields_ = [("embed_tokens", C.c_void_p), ("layers", LayerWeights * MAX_LAYERS),
+                ("norm", C.c_void_p)]
 
 
 class Context:
@@ -276,6 +295,11 @@ class Context:
 
     def qkv_proj_device(self, x, wq, wk, wv, q, k, v):
         _check(lib().g3attn_qkv_proj_device(self._h, x, wq, wk, wv, q, k, v))
+
+    def forward_device(self, weights: "Weights", token, pos, logits, compute_logits=True,
+                       hidden_out=None):
+        _check(lib().g3attn_forward_device(self._h, C.byref(weights), token, pos, logits,
+                                           int(compute_logits), hidden_out))
 
     def layer_attention_device(self, layer, pos, x, wq, wk, wv, wo, q_norm, k_norm, out):
         _check(lib().g3attn_layer_attention_device(self._h, layer, pos, x, wq, wk, wv, wo, q_norm,

@@ -111,6 +111,9 @@ struct g3attn_ctx {
     /* layer_attention scratch: q | k | v | attn of one token */
     float *d_la;
     size_t d_la_cap;
+    /* token forward activations: x | x_norm | proj | mlp | h (see forward) */
+    float *d_fw;
+    size_t d_fw_cap;
     /* prefill: staging sets *d_vflag = pf_epoch when a value is not exactly
      * bf16 (the attention kernel then adds its V_lo pass) */
     int *d_vflag;
@@ -161,6 +164,7 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_pf);
     hipFree(c->d_vflag);
     hipFree(c->d_la);
+    hipFree(c->d_fw);
     if (c->h_in) hipHostFree(c->h_in);
     if (c->h_out) hipHostFree(c->h_out);
     if (c->stream) hipStreamDestroy(c->stream);
@@ -917,6 +921,132 @@ int g3attn_layer_attention_device(g3attn_ctx *c, int layer, int pos, const float
     rc = g3attn_decode_device(c, layer, pos, q, k, v, q_norm, k_norm, attn);
     if (rc) return rc;
     return g3attn_matvec_bf16_device(c, out, wo, attn, c->cfg.hidden_size, qs);
+}
+
+/* ------------------------------------------------------------------ token forward */
+
+static int grow_buf(g3attn_ctx *c, float **p, size_t *cap, size_t bytes, const char *what) {
+    if (bytes <= *cap) return G3_OK;
+    HIP_TRY(hipStreamSynchronize(c->stream), what);
+    hipFree(*p);
+    *p = NULL;
+    *cap = 0;
+    if (!alloc_dev((void **)p, bytes, what)) return G3_ERR_OUT_OF_MEMORY;
+    *cap = bytes;
+    return G3_OK;
+}
+
+static int layer_step(g3attn_ctx *c, int op, float *x, float *t, float *y, const uint16_t *w_post,
+                      const uint16_t *w_next, const uint16_t *embed, int token) {
+    g3k_layer_args a;
+    memset(&a, 0, sizeof a);
+    a.op = op;
+    a.n = c->cfg.hidden_size;
+    a.token = token;
+    a.eps = c->cfg.rmsnorm_eps;
+    a.embed = embed;
+    a.w_post = w_post;
+    a.w_next = w_next;
+    a.x = x;
+    a.t = t;
+    a.y = y;
+    const int rc = g3k_layer_step(&a, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_forward_device step");
+    return G3_OK;
+}
+
+static int gemv(g3attn_ctx *c, float *y, const uint16_t *A, const float *x, int M, int K) {
+    g3k_matvec_args a;
+    memset(&a, 0, sizeof a);
+    a.x = x;
+    a.K = K;
+    a.n_mat = 1;
+    a.A[0] = A;
+    a.y[0] = y;
+    a.M[0] = M;
+    const int rc = g3k_matvec(&a, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_forward_device GEMV");
+    return G3_OK;
+}
+
+int g3attn_forward_device(g3attn_ctx *c, const g3attn_weights *w, int token_id, int pos,
+                          float *logits, int compute_logits, float *hidden_out) {
+    if (!c || !w || !w->embed_tokens || (compute_logits && (!logits || !w->norm))) {
+        set_err("g3attn_forward_device: null context, weights or output");
+        return G3_ERR_INVALID_ARG;
+    }
+    const g3attn_config *cfg = &c->cfg;
+    const int hid = cfg->hidden_size, inter = cfg->intermediate_size, L = cfg->num_layers;
+    if (token_id < 0 || token_id >= cfg->vocab_size || L < 1 || L > G3ATTN_MAX_LAYERS ||
+        hid < 1 || hid > G3K_LAYER_MAX_HIDDEN || inter < 1) {
+        set_err("g3attn_forward_device: token %d / vocab %d, layers %d, hidden %d, intermediate %d "
+                "out of range", token_id, cfg->vocab_size, L, hid, inter);
+        return G3_ERR_INVALID_ARG;
+    }
+    for (int l = 0; l < L; l++) {
+        const g3attn_layer_weights *lw = &w->layers[l];
+        if (!lw->input_layernorm || !lw->q_proj || !lw->k_proj || !lw->v_proj || !lw->o_proj ||
+            !lw->gate_proj || !lw->up_proj || !lw->down_proj) {
+            set_err("g3attn_forward_device: layer %d has a null projection or input norm", l);
+            return G3_ERR_INVALID_ARG;
+        }
+    }
+    if (pos < 0 || pos >= c->max_context) {
+        set_err("g3attn_forward_device: pos %d outside [0, %d)", pos, c->max_context);
+        return pos < 0 ? G3_ERR_INVALID_ARG : G3_ERR_CONTEXT_OVERFLOW;
+    }
+    hipSetDevice(c->device);
+    const size_t hb = align256((size_t)hid * 4);
+    int rc = grow_buf(c, &c->d_fw, &c->d_fw_cap, 4 * hb + align256((size_t)inter * 4), "forward activations");
+    if (rc) return rc;
+    const int qs = cfg->num_heads * D, ks = cfg->num_kv_heads * D;
+    rc = grow_buf(c, &c->d_la, &c->d_la_cap, (size_t)(2 * qs + 2 * ks) * sizeof(float), "layer scratch");
+    if (rc) return rc;
+    unsigned char *b = (unsigned char *)c->d_fw;
+    float *x = (float *)b, *xn = (float *)(b + hb), *proj = (float *)(b + 2 * hb);
+    float *mlp = (float *)(b + 3 * hb), *h = (float *)(b + 4 * hb);
+    float *q = c->d_la, *k = q + qs, *v = k + ks, *attn = v + ks;
+
+    /* embedding * sqrt(hidden) (:415-422), then layer 0's input norm (:444-446) */
+    if ((rc = layer_step(c, G3K_OP_EMBED, x, NULL, NULL, NULL, NULL, w->embed_tokens, token_id))) return rc;
+    if ((rc = layer_step(c, G3K_OP_NORM, x, NULL, xn, NULL, w->layers[0].input_layernorm, NULL, 0))) return rc;
+    for (int l = 0; l < L; l++) {
+        const g3attn_layer_weights *lw = &w->layers[l];
+        /* layer_attention (:449-460) */
+        if ((rc = g3attn_qkv_proj_device(c, xn, lw->q_proj, lw->k_proj, lw->v_proj, q, k, v))) return rc;
+        if ((rc = g3attn_decode_device(c, l, pos, q, k, v, lw->q_norm, lw->k_norm, attn))) return rc;
+        if ((rc = gemv(c, proj, lw->o_proj, attn, hid, qs))) return rc;
+        /* post-attention norm, residual, pre-feedforward norm (:463-477) */
+        if ((rc = layer_step(c, G3K_OP_RESIDUAL, x, proj, xn, lw->post_attention_layernorm,
+                             lw->pre_feedforward_layernorm, NULL, 0)))
+            return rc;
+        /* layer_mlp (:480-487, 369-388): gate and up GEMVs with gelu(gate) * up, down GEMV */
+        g3k_matvec_args a;
+        memset(&a, 0, sizeof a);
+        a.x = xn;
+        a.K = hid;
+        a.n_mat = 2;
+        a.mode = G3K_MV_GEGLU;
+        a.A[0] = lw->gate_proj;
+        a.A[1] = lw->up_proj;
+        a.y[0] = h;
+        a.M[0] = a.M[1] = inter;
+        if ((rc = g3k_matvec(&a, c->stream))) return hip_fail((hipError_t)rc, "g3attn_forward_device MLP");
+        if ((rc = gemv(c, mlp, lw->down_proj, h, hid, inter))) return rc;
+        /* post-feedforward norm, residual (:490-496); then the next layer's
+         * input norm, or the final norm before the logits (:508) */
+        const int last = l + 1 == L;
+        const uint16_t *w_next = last ? (compute_logits ? w->norm : NULL) : w->layers[l + 1].input_layernorm;
+        if ((rc = layer_step(c, G3K_OP_RESIDUAL, x, mlp, (last && !compute_logits) ? NULL : xn,
+                             lw->post_feedforward_layernorm, w_next, NULL, 0)))
+            return rc;
+    }
+    /* tied-embedding logits (:511) */
+    if (compute_logits && (rc = gemv(c, logits, w->embed_tokens, xn, cfg->vocab_size, hid))) return rc;
+    if (hidden_out)
+        HIP_TRY(hipMemcpyAsync(hidden_out, x, (size_t)hid * 4, hipMemcpyDeviceToDevice, c->stream),
+                "g3attn_forward_device hidden");
+    return G3_OK;
 }
 
 /* ------------------------------------------------------------------ gemma3_gqa */

@@ -177,6 +177,48 @@ int g3attn_layer_attention_device(g3attn_ctx *ctx, int layer, int pos, const flo
                                   const uint16_t *wo, const uint16_t *q_norm, const uint16_t *k_norm,
                                   float *out);
 
+/* Device copies of a model's bf16 tensors, field for field the layout of the
+ * reference's gemma3_weights_t (gemma3_transformer.c:56-74; the safetensors
+ * loader fills the host one, gemma3_safetensors.c:620-635): a caller that
+ * uploaded every tensor can fill this struct with the device addresses in the
+ * same places.  Entries of layers beyond cfg.num_layers are ignored. */
+#define G3ATTN_MAX_LAYERS 34
+typedef struct {
+    const uint16_t *input_layernorm;
+    const uint16_t *q_proj;
+    const uint16_t *k_proj;
+    const uint16_t *v_proj;
+    const uint16_t *o_proj;
+    const uint16_t *q_norm;
+    const uint16_t *k_norm;
+    const uint16_t *post_attention_layernorm;
+    const uint16_t *gate_proj;
+    const uint16_t *up_proj;
+    const uint16_t *down_proj;
+    const uint16_t *pre_feedforward_layernorm;
+    const uint16_t *post_feedforward_layernorm;
+} g3attn_layer_weights;
+
+typedef struct {
+    const uint16_t *embed_tokens;
+    g3attn_layer_weights layers[G3ATTN_MAX_LAYERS];
+    const uint16_t *norm;
+} g3attn_weights;
+
+/* One token through the whole model: gemma3_transformer_forward
+ * (gemma3_transformer.c:396-512) on the GPU.  Embedding row * sqrt(hidden);
+ * per layer the input RMSNorm, layer_attention (projections, QK-norm, RoPE,
+ * cache write at pos, GQA, o_proj), post-attention RMSNorm + residual,
+ * pre-feedforward RMSNorm, the GELU-gated MLP and the post-feedforward
+ * RMSNorm + residual; then, if compute_logits, the final RMSNorm and the
+ * tied-embedding logits [vocab_size].  Norm weights may be NULL where the
+ * reference allows it (post-attention, pre- / post-feedforward).  hidden_out
+ * (optional, [hidden_size]) receives the final hidden state before the final
+ * norm.  weights is a host struct of device pointers; logits / hidden_out are
+ * device buffers.  Enqueued on the context stream. */
+int g3attn_forward_device(g3attn_ctx *ctx, const g3attn_weights *weights, int token_id, int pos,
+                          float *logits, int compute_logits, float *hidden_out);
+
 /* The context's HIP stream (hipStream_t), for callers that interleave their
  * own work; and a wait for everything queued on it. */
 void *g3attn_stream(g3attn_ctx *ctx);

@@ -124,6 +124,15 @@ void g3o_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K) 
     for (int i = 0; i < M; i++) y[i] = matvec_row(A + (size_t)i * K, x, K);
 }
 
+/* gemma3_kernels.c:348-357.  GELU, tanh approximation, in place. */
+void g3o_gelu_tanh(float *x, int n) {
+    const float c0 = 0.7978845608028654f, c1 = 0.044715f;   /* sqrt(2/pi); the cubic term */
+    for (int i = 0; i < n; i++) {
+        const float v = x[i];
+        x[i] = 0.5f * v * (1.0f + tanhf(c0 * (v + c1 * (v * v * v))));
+    }
+}
+
 /* gemma3_kernels.c:396-415.  Max, exp(x - max) with running sum, scale by 1/sum. */
 void g3o_softmax(float *x, int n) {
     float m = x[0];
@@ -490,4 +499,93 @@ uint64_t g3o_fnv1a64(const void *data, size_t nbytes) {
         h *= 0x100000001b3ull;
     }
     return h;
+}
+
+
+/* ---------------------------------------------------------------- token forward */
+
+/* gemma3_transformer.c:396-512 with layer_mlp (:362-391), for a sequence of
+ * tokens from an empty cache (positions 0..n-1). */
+int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
+                    const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                    const g3o_model *m) {
+    const int H = m->hidden_size, I = m->intermediate_size, V = m->vocab_size, L = m->num_layers;
+    const int d = m->head_dim, qs = m->num_heads * d, ks = m->num_kv_heads * d;
+    g3o_config cfg;
+    cfg.num_layers = L;
+    cfg.num_heads = m->num_heads;
+    cfg.num_kv_heads = m->num_kv_heads;
+    cfg.head_dim = d;
+    cfg.max_context = m->max_context;
+    cfg.sliding_window = m->sliding_window;
+    cfg.rmsnorm_eps = m->rmsnorm_eps;
+    cfg.rope_theta_local = m->rope_theta_local;
+    cfg.rope_theta_global = m->rope_theta_global;
+    const int cap = m->max_context > m->sliding_window ? m->max_context : m->sliding_window;
+    float *x = malloc((size_t)H * 4), *xn = malloc((size_t)H * 4), *proj = malloc((size_t)H * 4);
+    float *mlp = malloc((size_t)H * 4), *q = malloc((size_t)qs * 4), *k = malloc((size_t)ks * 4);
+    float *v = malloc((size_t)ks * 4), *attn = malloc((size_t)qs * 4);
+    float *gate = malloc((size_t)I * 4), *up = malloc((size_t)I * 4);
+    float *work = malloc((size_t)2 * cap * 4);
+    float *rl = malloc((size_t)m->max_context * d * 4), *rg = malloc((size_t)m->max_context * d * 4);
+    float **kc = calloc((size_t)L, sizeof(float *)), **vc = calloc((size_t)L, sizeof(float *));
+    int rc = 0;
+    if (!x || !xn || !proj || !mlp || !q || !k || !v || !attn || !gate || !up || !work || !rl || !rg ||
+        !kc || !vc) {
+        rc = -4;
+        goto done;
+    }
+    for (int l = 0; l < L; l++) {
+        const size_t rows = g3o_is_global_layer(l) ? (size_t)m->max_context : (size_t)m->sliding_window;
+        kc[l] = calloc(rows * ks, 4);
+        vc[l] = calloc(rows * ks, 4);
+        if (!kc[l] || !vc[l]) {
+            rc = -4;
+            goto done;
+        }
+    }
+    g3o_rope_precompute(rl, m->max_context, d, m->rope_theta_local);
+    g3o_rope_precompute(rg, m->max_context, d, m->rope_theta_global);
+    const float escale = sqrtf((float)H);
+    for (int i = 0; i < n && !rc; i++) {
+        const int pos = i;
+        for (int j = 0; j < H; j++) x[j] = g3o_bf16_to_f32(embed[(size_t)tokens[i] * H + j]) * escale;
+        for (int l = 0; l < L && !rc; l++) {
+            const uint16_t *const *t = layer_w + (size_t)l * 13;
+            g3o_rmsnorm_bf16(xn, x, t[0], H, m->rmsnorm_eps);
+            g3o_matvec_bf16(q, t[1], xn, qs, H);
+            g3o_matvec_bf16(k, t[2], xn, ks, H);
+            g3o_matvec_bf16(v, t[3], xn, ks, H);
+            rc = g3o_layer_decode(attn, q, k, v, t[5], t[6], kc[l], vc[l],
+                                  g3o_is_global_layer(l) ? rg : rl, &cfg, l, pos, work);
+            if (rc) break;
+            g3o_matvec_bf16(proj, t[4], attn, H, qs);
+            if (t[7]) g3o_rmsnorm_bf16(proj, proj, t[7], H, m->rmsnorm_eps);
+            for (int j = 0; j < H; j++) x[j] = x[j] + proj[j];
+            if (t[11])
+                g3o_rmsnorm_bf16(xn, x, t[11], H, m->rmsnorm_eps);
+            else
+                memcpy(xn, x, (size_t)H * 4);
+            g3o_matvec_bf16(gate, t[8], xn, I, H);
+            g3o_matvec_bf16(up, t[9], xn, I, H);
+            g3o_gelu_tanh(gate, I);
+            for (int j = 0; j < I; j++) gate[j] = gate[j] * up[j];
+            g3o_matvec_bf16(mlp, t[10], gate, H, I);
+            if (t[12]) g3o_rmsnorm_bf16(mlp, mlp, t[12], H, m->rmsnorm_eps);
+            for (int j = 0; j < H; j++) x[j] = x[j] + mlp[j];
+        }
+        if (rc) break;
+        g3o_rmsnorm_bf16(xn, x, norm, H, m->rmsnorm_eps);
+        g3o_matvec_bf16(logits + (size_t)i * V, embed, xn, V, H);
+    }
+    if (!rc) memcpy(hidden_last, x, (size_t)H * 4);
+done:
+    if (kc)
+        for (int l = 0; l < L; l++) free(kc[l]);
+    if (vc)
+        for (int l = 0; l < L; l++) free(vc[l]);
+    free(kc); free(vc);
+    free(x); free(xn); free(proj); free(mlp); free(q); free(k); free(v); free(attn);
+    free(gate); free(up); free(work); free(rl); free(rg);
+    return rc;
 }

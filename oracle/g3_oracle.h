@@ -21,6 +21,8 @@
  *   g3o_prefill_mt / g3o_prefill_rows        the same loop, tokens in parallel
  *   g3o_is_global_layer / g3o_layer_theta    gemma3.h:347-360
  *   g3o_matvec_bf16                          gemma3_kernels.c:146-238 (AVX2 order)
+ *   g3o_gelu_tanh                            gemma3_kernels.c:348-357
+ *   g3o_forward_seq                          gemma3_transformer.c:396-512 (+ layer_mlp :362-391)
  *
  * How each function is pinned (tests/test_oracle_*.py):
  *   - against golden vectors written by the real reference sources compiled
@@ -86,6 +88,29 @@ void g3o_gqa_rows(float *out, const float *q, const float *k, const float *v,
  * 16 elements, one over a remaining block of 8, lane sums combined as
  * (acc0 + acc1) -> halves -> pairs -> one, then a scalar tail. */
 void g3o_matvec_bf16(float *y, const uint16_t *A, const float *x, int M, int K);
+
+/* gemma3_gelu_tanh_inplace: x = 0.5 x (1 + tanhf(sqrt(2/pi) (x + 0.044715 x^3))). */
+void g3o_gelu_tanh(float *x, int n);
+
+/* Shape of a whole model for g3o_forward_seq (gemma3_config fields). */
+typedef struct {
+    int vocab_size, hidden_size, intermediate_size, num_layers;
+    int num_heads, num_kv_heads, head_dim, max_context, sliding_window;
+    float rmsnorm_eps, rope_theta_local, rope_theta_global;
+} g3o_model;
+
+/* gemma3_transformer_forward for tokens[0..n-1] at positions 0..n-1 from an
+ * empty cache: per step the embedding row * sqrt(hidden), then per layer the
+ * input RMSNorm, the Q/K/V GEMVs, the attention section (g3o_layer_decode),
+ * the o_proj GEMV, post-attention RMSNorm + residual, pre-feedforward RMSNorm
+ * (or a copy when absent), gate / up GEMVs, gelu(gate) * up, the down GEMV,
+ * post-feedforward RMSNorm + residual; then the final RMSNorm and the
+ * tied-embedding logits.  layer_w: num_layers x 13 tensors in the
+ * gemma3_weights_t field order (post-attention, pre- and post-feedforward
+ * norms may be NULL).  logits [n][vocab]; hidden_last [hidden]. */
+int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
+                    const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                    const g3o_model *m);
 
 /* cache_kv: copies k, v (kv_size floats each) into slot pos or pos % window. */
 void g3o_cache_kv(float *k_cache, float *v_cache, const float *k, const float *v,

@@ -38,6 +38,16 @@ class _Cfg(C.Structure):
     ]
 
 
+class _Model(C.Structure):
+    _fields_ = [
+        ("vocab_size", C.c_int), ("hidden_size", C.c_int), ("intermediate_size", C.c_int),
+        ("num_layers", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int),
+        ("head_dim", C.c_int), ("max_context", C.c_int), ("sliding_window", C.c_int),
+        ("rmsnorm_eps", C.c_float), ("rope_theta_local", C.c_float),
+        ("rope_theta_global", C.c_float),
+    ]
+
+
 @dataclass
 class Config:
     """gemma3_config subset (gemma3.h:82-95) read by the attention path."""
@@ -107,6 +117,10 @@ def lib():
                                           C.c_int, C.c_float, C.c_int]
         L.g3o_gen_normal_bf16.argtypes = [_f32p, C.c_size_t, C.c_uint64, C.c_size_t, C.c_int]
         L.g3o_matvec_bf16.argtypes = [_f32p, _u16p, _f32p, C.c_int, C.c_int]
+        L.g3o_gelu_tanh.argtypes = [_f32p, C.c_int]
+        L.g3o_forward_seq.argtypes = [_f32p, _f32p, _i32p, C.c_int, _u16p, C.c_void_p, _u16p,
+                                      C.POINTER(_Model)]
+        L.g3o_forward_seq.restype = C.c_int
         L.g3o_splitmix64.argtypes = [C.c_uint64, C.c_uint64]
         L.g3o_splitmix64.restype = C.c_uint64
         L.g3o_fnv1a64.argtypes = [C.c_void_p, C.c_size_t]
@@ -156,6 +170,10 @@ def ref():
                                           C.c_void_p, _f32p, _f32p, _f32p, C.c_int, C.c_int,
                                           C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
         R.ref_layer_attention.restype = C.c_int
+        R.ref_forward_seq.argtypes = [_f32p, _f32p, _i32p, C.c_int, _u16p, C.c_void_p, _u16p,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, C.c_int]
+        R.ref_forward_seq.restype = C.c_int
         _ref = R
     return _ref
 
@@ -261,6 +279,55 @@ def layer_attention(cfg: Config, layer: int, pos: int, x, wq, wk, wv, wo, k_cach
     q, k, v = matvec_bf16(wq, x), matvec_bf16(wk, x), matvec_bf16(wv, x)
     attn, _, _ = layer_decode(cfg, layer, pos, q, k, v, k_cache, v_cache, table, q_norm, k_norm)
     return matvec_bf16(wo, attn)
+
+
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    """gemma3_gelu_tanh_inplace (gemma3_kernels.c:348-357) on a copy of x."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    lib().g3o_gelu_tanh(y, y.size)
+    return y
+
+
+# the 13 per-layer tensors in gemma3_weights_t order (gemma3.h)
+LAYER_TENSORS = ("input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
+                 "post_attention_layernorm", "gate_proj", "up_proj", "down_proj",
+                 "pre_feedforward_layernorm", "post_feedforward_layernorm")
+
+
+def forward_seq(cfg: Config, hidden: int, inter: int, tokens, embed: np.ndarray, layers,
+                norm: np.ndarray, use_ref=False):
+    """gemma3_transformer_forward (gemma3_transformer.c:396-512) for tokens at
+    positions 0..n-1 from an empty cache.  ``layers`` is a list of
+    cfg.num_layers dicts keyed by LAYER_TENSORS (bf16 uint16 arrays; the
+    norms other than input_layernorm may be None).  ``embed`` is
+    [vocab][hidden] bf16 (tied with the logits).  Returns (logits [n][vocab]
+    fp32, hidden state after the last token [hidden])."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    vocab = embed.size // hidden
+    assert embed.size == vocab * hidden and len(layers) == cfg.num_layers
+    keep = []
+    ptrs = (C.c_void_p * (13 * cfg.num_layers))()
+    for l, lw in enumerate(layers):
+        for j, name in enumerate(LAYER_TENSORS):
+            a = lw.get(name)
+            if a is not None:
+                a = np.ascontiguousarray(a, dtype=np.uint16)
+                keep.append(a)
+                ptrs[13 * l + j] = a.ctypes.data
+    logits = np.empty((tokens.size, vocab), dtype=np.float32)
+    hid = np.empty(hidden, dtype=np.float32)
+    if use_ref:
+        rc = ref().ref_forward_seq(logits, hid, tokens, tokens.size, embed, ptrs, norm, vocab,
+                                   hidden, inter, cfg.num_layers, cfg.num_heads, cfg.num_kv_heads,
+                                   cfg.max_context, cfg.sliding_window)
+    else:
+        m = _Model(vocab, hidden, inter, cfg.num_layers, cfg.num_heads, cfg.num_kv_heads,
+                   cfg.head_dim, cfg.max_context, cfg.sliding_window, cfg.rmsnorm_eps,
+                   cfg.rope_theta_local, cfg.rope_theta_global)
+        rc = lib().g3o_forward_seq(logits, hid, tokens, tokens.size, embed, ptrs, norm, C.byref(m))
+    if rc:
+        raise RuntimeError(f"forward_seq rc={rc}")
+    return logits, hid
 
 
 def layer_decode(cfg: Config, layer: int, pos: int, q, k, v, k_cache, v_cache, table,

@@ -147,6 +147,61 @@ done:
     return rc;
 }
 
+/* gemma3_transformer_forward (gemma3_transformer.c:396-512) itself, run for
+ * tokens[0..n-1] at positions 0..n-1 from an empty cache, with caller-given
+ * bf16 weights (layer_w: num_layers x 13 tensors in the gemma3_weights_t
+ * field order) and model shape.  logits [n][vocab] holds every step's
+ * logits; hidden_last [hidden] the hidden state after the last step. */
+int ref_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
+                    const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                    int vocab, int hidden, int inter, int num_layers, int hq, int hkv,
+                    int max_context, int window) {
+    if (num_layers < 1 || num_layers > GEMMA3_NUM_LAYERS) return -1;
+    gemma3_config cfg = harness_cfg(hq, hkv, max_context, window);
+    cfg.vocab_size = vocab;
+    cfg.hidden_size = hidden;
+    cfg.intermediate_size = inter;
+    cfg.num_layers = num_layers;
+    gemma3_weights_t w;
+    memset(&w, 0, sizeof w);
+    w.embed_tokens = embed;
+    w.norm = norm;
+    for (int l = 0; l < num_layers; l++) {
+        const uint16_t *const *t = layer_w + (size_t)l * 13;
+        w.layers[l].input_layernorm = t[0];
+        w.layers[l].q_proj = t[1];
+        w.layers[l].k_proj = t[2];
+        w.layers[l].v_proj = t[3];
+        w.layers[l].o_proj = t[4];
+        w.layers[l].q_norm = t[5];
+        w.layers[l].k_norm = t[6];
+        w.layers[l].post_attention_layernorm = t[7];
+        w.layers[l].gate_proj = t[8];
+        w.layers[l].up_proj = t[9];
+        w.layers[l].down_proj = t[10];
+        w.layers[l].pre_feedforward_layernorm = t[11];
+        w.layers[l].post_feedforward_layernorm = t[12];
+    }
+    gemma3_kv_cache *cache = gemma3_kv_cache_alloc(&cfg, max_context);
+    activation_buffers *buf = alloc_buffers(&cfg);
+    float *rl = (float *)malloc((size_t)max_context * RH_D * 4);
+    float *rg = (float *)malloc((size_t)max_context * RH_D * 4);
+    int rc = 0;
+    if (!cache || !buf || !rl || !rg) { rc = -4; goto done; }
+    gemma3_rope_precompute(rl, max_context, RH_D, cfg.rope_theta_local);
+    gemma3_rope_precompute(rg, max_context, RH_D, cfg.rope_theta_global);
+    for (int i = 0; i < n && !rc; i++)
+        rc = gemma3_transformer_forward(logits + (size_t)i * vocab, tokens[i], i, &w, cache, buf, &cfg, 1,
+                                        rl, rg, NULL);
+    if (!rc) memcpy(hidden_last, buf->x, (size_t)hidden * 4);
+done:
+    if (cache) gemma3_kv_cache_free(cache);
+    if (buf) free_buffers(buf);
+    free(rl);
+    free(rg);
+    return rc;
+}
+
 /* The per-token prefill attention loop of gemma3_transformer.c:641-692, on the
  * reference's own functions.  Q, K are modified in place (normed + RoPE'd). */
 int ref_prefill_loop(float *attn_out, float *Q, float *K, const float *V,

@@ -234,6 +234,62 @@ def matvec_fixture():
     return out
 
 
+# A small model of Gemma 3's structure for the whole-token forward: 6 layers
+# (layer 5 global), 8 query / 4 KV heads of 256, a 16-row sliding window that
+# the 40-token sequence wraps.  Layer 3 drops its optional norms (q_norm,
+# k_norm, post-attention, pre- and post-feedforward), which the reference
+# skips when NULL.
+FORWARD = dict(hidden=512, inter=1536, vocab=1024, n=40, layers=6, max_context=64, window=16)
+FORWARD_ROWS = (0, 5, 15, 16, 17, 31, 39)   # the logits rows kept in the fixture
+
+
+def norm_bf16(n, seed):
+    """Small per-channel RMSNorm weights w (gain 1 + w): N(0,1) * 2^-3 in bf16."""
+    a = (O.gen_normal_bf16(n, seed) * np.float32(0.125)).astype(np.float32)
+    return (a.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def forward_case(**over):
+    f = dict(FORWARD, **over)
+    H, I, V, L = f["hidden"], f["inter"], f["vocab"], f["layers"]
+    cfg = O.Config(num_layers=L, max_context=f["max_context"], sliding_window=f["window"])
+    qs, ks = cfg.num_heads * 256, cfg.num_kv_heads * 256
+    embed = weights_bf16(V, H, 0xF000)
+    layers = []
+    for l in range(L):
+        s = 0xF100 + 32 * l
+        lw = dict(input_layernorm=norm_bf16(H, s), q_proj=weights_bf16(qs, H, s + 1),
+                  k_proj=weights_bf16(ks, H, s + 2), v_proj=weights_bf16(ks, H, s + 3),
+                  o_proj=weights_bf16(H, qs, s + 4), q_norm=norm_bf16(256, s + 5),
+                  k_norm=norm_bf16(256, s + 6), post_attention_layernorm=norm_bf16(H, s + 7),
+                  gate_proj=weights_bf16(I, H, s + 8), up_proj=weights_bf16(I, H, s + 9),
+                  down_proj=weights_bf16(H, I, s + 10), pre_feedforward_layernorm=norm_bf16(H, s + 11),
+                  post_feedforward_layernorm=norm_bf16(H, s + 12))
+        if l == 3:
+            for k in ("q_norm", "k_norm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                      "post_feedforward_layernorm"):
+                lw[k] = None
+        layers.append(lw)
+    norm = norm_bf16(H, 0xFF00)
+    tokens = np.random.default_rng(0xF0F0).integers(0, V, f["n"]).astype(np.int32)
+    return cfg, f, embed, layers, norm, tokens
+
+
+def forward_hash(embed, layers, norm, tokens):
+    parts = [h64(embed), h64(norm), h64(tokens)]
+    for lw in layers:
+        parts += [h64(a) if a is not None else np.uint64(0) for a in (lw[k] for k in O.LAYER_TENSORS)]
+    return np.array(parts, np.uint64)
+
+
+def forward_fixture():
+    cfg, f, embed, layers, norm, tokens = forward_case()
+    logits, hid = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm, use_ref=True)
+    return {"in_hash": forward_hash(embed, layers, norm, tokens),
+            "rows": np.array(FORWARD_ROWS, np.int32), "logits": logits[list(FORWARD_ROWS)],
+            "argmax": logits.argmax(axis=1).astype(np.int32), "hidden": hid}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--no-big", action="store_true")
@@ -243,7 +299,8 @@ def main():
         sys.exit("oracle/_ref/libg3ref.so is not built (needs /root/reference at build time)")
     ap_only = set(filter(None, args.only.split(",")))
     for name, fn in (("rope", rope_fixture), ("kernels", kernels_fixture), ("decode", decode_fixture),
-                     ("prefill", lambda: prefill_fixture(not args.no_big)), ("matvec", matvec_fixture)):
+                     ("prefill", lambda: prefill_fixture(not args.no_big)), ("matvec", matvec_fixture),
+                     ("forward", forward_fixture)):
         if ap_only and name not in ap_only:
             continue
         t0 = time.time()

@@ -468,3 +468,101 @@ def test_matvec_restatement_equals_reference_build_random():
         x = rng.standard_normal(K).astype(np.float32)
         y, yr = O.matvec_bf16(A, x), O.matvec_bf16(A, x, use_ref=True)
         assert np.all(np.abs(y - yr) <= 4 * _matvec_bound(A, x) / K * 16), (M, K)
+
+
+# ---------------------------------------------------------------- token forward
+
+def _gelu64(x):
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def test_gelu_known_values_and_odd_identity():
+    """gemma3_gelu_tanh_inplace: gelu(0) = 0; gelu(x) - gelu(-x) = x exactly in
+    real arithmetic (0.5x(1 + t) + 0.5x(1 - t)); the tanh form's published
+    values at 1 and -1 (0.8411920, -0.1588080); gelu -> x and -> 0 in the tails."""
+    x = np.linspace(-8, 8, 4001).astype(np.float32)
+    y = O.gelu_tanh(x).astype(np.float64)
+    assert O.gelu_tanh(np.zeros(1, np.float32))[0] == 0.0
+    neg = O.gelu_tanh(-x).astype(np.float64)
+    assert np.all(np.abs((y - neg) - x) <= 2e-6 * np.maximum(1.0, np.abs(x)))
+    g1 = O.gelu_tanh(np.array([1.0, -1.0], np.float32))
+    assert abs(g1[0] - 0.8411920) < 1e-6 and abs(g1[1] + 0.1588080) < 1e-6
+    assert np.all(np.abs(y - _gelu64(x.astype(np.float64))) <= 1e-6 * np.maximum(1.0, np.abs(x)))
+    assert abs(y[-1] - 8.0) < 1e-6 and abs(y[0]) < 1e-6
+    # the exact-erf GELU and SiLU differ by far more than the bound above
+    silu = x / (1 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(y - silu)) > 1e-2
+
+
+def _bf64(a):
+    return (np.asarray(a).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _forward_pos0_64(cfg, f, embed, layers, norm, token, mutant=None):
+    """fp64 forward of the first token (position 0): every attention softmax
+    is over one row, so each head's output is its KV head's V row and neither
+    RoPE nor the QK norms enter.  What is left pins the embedding scale, the
+    (1 + w) norms, the residual structure, the GQA head map, the gelu(gate) *
+    up MLP and the tied logits; ``mutant`` names one plausible mistake."""
+    H = f["hidden"]
+    E = _bf64(embed).reshape(-1, H)
+
+    def rms(x, w):
+        gain = _bf64(w) if mutant == "gain_w" else 1.0 + _bf64(w)
+        return x / np.sqrt((x * x).mean() + 1e-6) * gain
+
+    x = E[token] * (1.0 if mutant == "no_embed_scale" else np.sqrt(H))
+    G = cfg.num_heads // cfg.num_kv_heads
+    for lw in layers:
+        xn = rms(x, lw["input_layernorm"])
+        v = (_bf64(lw["v_proj"]) @ xn).reshape(cfg.num_kv_heads, 256)
+        kv = [h % cfg.num_kv_heads if mutant == "head_map" else h // G for h in range(cfg.num_heads)]
+        proj = _bf64(lw["o_proj"]) @ v[kv].reshape(-1)
+        if lw["post_attention_layernorm"] is not None and mutant != "no_post_attn":
+            proj = rms(proj, lw["post_attention_layernorm"])
+        x = x + proj
+        xn = rms(x, lw["pre_feedforward_layernorm"]) if lw["pre_feedforward_layernorm"] is not None else x
+        gate, up = _bf64(lw["gate_proj"]) @ xn, _bf64(lw["up_proj"]) @ xn
+        h = gate * _gelu64(up) if mutant == "gelu_on_up" else _gelu64(gate) * up
+        mlp = _bf64(lw["down_proj"]) @ h
+        if lw["post_feedforward_layernorm"] is not None:
+            mlp = rms(mlp, lw["post_feedforward_layernorm"])
+        x = x + mlp
+    return E @ rms(x, norm), x
+
+
+def test_forward_first_token_closed_form_and_mutants():
+    MG = _mg()
+    cfg, f, embed, layers, norm, tokens = MG.forward_case(n=1)
+    logits, hid = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm)
+    want, xw = _forward_pos0_64(cfg, f, embed, layers, norm, int(tokens[0]))
+    scale = np.sqrt((want ** 2).mean())
+    bar = 2e-5 * scale
+    assert np.max(np.abs(logits[0] - want)) <= bar
+    assert np.max(np.abs(hid - xw)) <= 2e-5 * np.sqrt((xw ** 2).mean())
+    for m in ("gain_w", "no_embed_scale", "head_map", "no_post_attn", "gelu_on_up"):
+        wm, _ = _forward_pos0_64(cfg, f, embed, layers, norm, int(tokens[0]), mutant=m)
+        assert np.max(np.abs(logits[0] - wm)) > 100 * bar, m
+
+
+def test_forward_matches_reference_golden():
+    """gemma3_transformer_forward over 40 tokens of a 6-layer model (window 16,
+    so the local layers' ring wraps; layer 3 without its optional norms)."""
+    MG = _mg()
+    g = gold("forward")
+    cfg, f, embed, layers, norm, tokens = MG.forward_case()
+    assert list(MG.forward_hash(embed, layers, norm, tokens)) == list(g["in_hash"])
+    logits, hid = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm)
+    assert rel(logits[list(g["rows"])], g["logits"]) < 1e-5
+    assert rel(hid, g["hidden"]) < 1e-5
+    assert np.array_equal(logits.argmax(axis=1), g["argmax"])
+
+
+@pytest.mark.skipif(not O.have_ref(), reason="oracle/_ref not built (no reference sources)")
+def test_forward_restatement_equals_reference_build_random():
+    MG = _mg()
+    cfg, f, embed, layers, norm, tokens = MG.forward_case(hidden=768, inter=1024, vocab=512, n=21,
+                                                          window=8, max_context=32)
+    a = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm)
+    b = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm, use_ref=True)
+    assert rel(a[0], b[0]) < 1e-5 and rel(a[1], b[1]) < 1e-5

@@ -486,8 +486,9 @@ def main():
         ctx.close()
         del Ws
 
-    # ---------------- next row: one token through the whole model (34 layers,
-    # tied logits) at configs[1]'s position, Gemma3-4B shapes, random weights
+    # ---------------- next rows: the model uploaded from host memory, then one
+    # token through the whole of it (34 layers, tied logits) at configs[1]'s
+    # position, Gemma3-4B shapes, random weights
     if not only or "forward" in only:
         torch = B.torch
         ctx = B.context(8192)
@@ -496,31 +497,45 @@ def main():
         cfg = ctx.cfg
         hid, inter, vocab, nl = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers
         assert (hid, inter, vocab, nl) == (2560, 10240, 262208, 34)
+        shapes = {"input_layernorm": hid, "q_proj": QS * hid, "k_proj": KS * hid, "v_proj": KS * hid,
+                  "o_proj": hid * QS, "q_norm": D, "k_norm": D, "post_attention_layernorm": hid,
+                  "gate_proj": inter * hid, "up_proj": inter * hid, "down_proj": hid * inter,
+                  "pre_feedforward_layernorm": hid, "post_feedforward_layernorm": hid}
+        total = vocab * hid + hid + nl * sum(shapes.values())
+        # host model: one pageable buffer (as a file mapping would be) tiled from a
+        # 64 MiB pool of seeded N(0,1) * 2^-6 bf16 values
+        pool_f = (np.random.default_rng(0x5EED).standard_normal(1 << 25) * 2.0 ** -6).astype(np.float32)
+        pool = (pool_f.view(np.uint32) >> 16).astype(np.uint16)
+        host = np.empty(total, np.uint16)
+        for o in range(0, total, pool.size):
+            n = min(pool.size, total - o)
+            host[o:o + n] = pool[:n]
+        HW, off = G.Weights(), 0
 
-        def wbf16(r, c):
-            return B.randn_bf16(r, c).mul_(2.0 ** -6).to(torch.bfloat16).view(torch.int16)
-
-        def nbf16(n):
-            return B.randn_bf16(n).mul_(0.125).to(torch.bfloat16).view(torch.int16)
-        keep = []
-        W = G.Weights()
-
-        def dev(t):
-            keep.append(t)
-            return t.data_ptr()
-        W.embed_tokens, W.norm = dev(wbf16(vocab, hid)), dev(nbf16(hid))
+        def take(n):
+            nonlocal off
+            p = host[off:off + n].ctypes.data
+            off += n
+            return p
+        HW.embed_tokens, HW.norm = take(vocab * hid), take(hid)
         for l in range(nl):
-            lw = W.layers[l]
-            lw.input_layernorm, lw.q_norm, lw.k_norm = dev(nbf16(hid)), dev(nbf16(D)), dev(nbf16(D))
-            lw.q_proj, lw.k_proj, lw.v_proj = dev(wbf16(QS, hid)), dev(wbf16(KS, hid)), dev(wbf16(KS, hid))
-            lw.o_proj = dev(wbf16(hid, QS))
-            lw.gate_proj, lw.up_proj = dev(wbf16(inter, hid)), dev(wbf16(inter, hid))
-            lw.down_proj = dev(wbf16(hid, inter))
-            lw.post_attention_layernorm = dev(nbf16(hid))
-            lw.pre_feedforward_layernorm = dev(nbf16(hid))
-            lw.post_feedforward_layernorm = dev(nbf16(hid))
+            for name, n in shapes.items():
+                setattr(HW.layers[l], name, take(n))
+        assert off == total
+        t0 = time.perf_counter()
+        ctx.upload_weights(HW)
+        up_s = time.perf_counter() - t0
+        del host
+        extra["weight_upload"] = {
+            "config": "g3attn_upload_weights of the whole Gemma3-4B-shaped model (every bf16 tensor, "
+                      "%.2f GB) from pageable host memory through two pinned 32 MiB staging buffers"
+                      % (2 * total / 1e9),
+            "s": round(up_s, 3),
+            "GB/s": round(2 * total / up_s / 1e9, 2),
+        }
+        log(f"[bench] upload: {extra['weight_upload']}")
+        W = ctx.device_weights()
         logits = torch.empty(vocab, device=B.dev)
-        assert keep[0].numel() == vocab * hid and logits.numel() == vocab
         torch.cuda.synchronize()
         pos = 8191
         layer_w = 2 * hid * (QS + 2 * KS) + 2 * hid * QS + 3 * 2 * hid * inter
@@ -536,8 +551,9 @@ def main():
         t = region / steps
         extra["forward_token_pos8191"] = {
             "config": "one token through all 34 layers + final norm + tied logits at pos 8191 "
-                      "(g3attn_forward_device), Gemma3-4B shapes (hidden 2560, intermediate 10240, "
-                      "vocab 262208), random bf16 weights (7.8 GB), cache rows before pos zero",
+                      "(g3attn_forward_device on the uploaded model), Gemma3-4B shapes (hidden 2560, "
+                      "intermediate 10240, vocab 262208), random bf16 weights, cache rows before "
+                      "pos zero",
             "ms_per_token": round(t * 1e3, 3),
             "tokens_per_s": round(1.0 / t, 1),
             "bytes_per_token": fwd_bytes,
@@ -545,8 +561,16 @@ def main():
             "frac_of_hbm_peak": round(fwd_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
         }
         log(f"[bench] forward: {extra['forward_token_pos8191']}")
+        # the backend hook's blocking call: host logits, one host round trip per token
+        for _ in range(3):
+            ctx.forward_token(2, pos)
+        t0 = time.perf_counter()
+        for _ in range(20):
+            lh = ctx.forward_token(2, pos)
+        t_host = (time.perf_counter() - t0) / 20
+        assert np.all(np.isfinite(lh))
+        extra["forward_token_pos8191"]["host_logits_ms_per_token"] = round(t_host * 1e3, 3)
         ctx.close()
-        del keep, W
 
     # ---------------- prefill.  The configs' inputs are
     # bf16-valued; the fp32 line feeds values off the bf16 grid, which takes the

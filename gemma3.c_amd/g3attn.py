@@ -29,6 +29,7 @@ ERR_CONTEXT_OVERFLOW = -8
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _vp = C.c_void_p
 
 
@@ -100,12 +101,18 @@ def lib():
     L.g3attn_layer_attention_device.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                                 _vp, _vp, _vp]
     L.g3attn_forward_device.argtypes = [_vp, C.c_void_p, C.c_int, C.c_int, _vp, C.c_int, _vp]
+    L.g3attn_upload_weights.argtypes = [_vp, C.c_void_p]
+    L.g3attn_device_weights.argtypes = [_vp]
+    L.g3attn_device_weights.restype = C.c_void_p
+    L.g3attn_forward_token.argtypes = [_vp, C.c_int, C.c_int, C.c_void_p, C.c_int]
+    L.g3attn_prefill_tokens.argtypes = [_vp, _i32p, C.c_int, C.c_int, C.c_void_p]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
                  "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
                  "g3attn_profile_enable", "g3attn_profile_read", "g3attn_matvec_bf16_device",
                  "g3attn_qkv_proj_device", "g3attn_layer_attention_device",
-                 "g3attn_forward_device"):
+                 "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
+                 "g3attn_prefill_tokens"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -186,6 +193,29 @@ class Weights(C.Structure):
     """g3attn_weights (the layout of the reference's gemma3_weights_t)."""
     _fields_ = [("embed_tokens", C.c_void_p), ("layers", LayerWeights * MAX_LAYERS),
                 ("norm", C.c_void_p)]
+
+
+LAYER_TENSORS = tuple(n for n, _ in LayerWeights._fields_)
+
+
+def host_weights(embed: np.ndarray, layers, norm: np.ndarray):
+    """A Weights of host addresses for upload_weights: ``layers`` is a list of
+    dicts keyed by LAYER_TENSORS (uint16 bf16 arrays, None where absent).
+    Returns (weights, arrays) - keep ``arrays`` alive until the upload returns."""
+    keep = []
+
+    def ptr(a):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=np.uint16)
+        keep.append(a)
+        return a.ctypes.data
+    W = Weights()
+    W.embed_tokens, W.norm = ptr(embed), ptr(norm)
+    for l, lw in enumerate(layers):
+        for name in LAYER_TENSORS:
+            setattr(W.layers[l], name, ptr(lw.get(name)))
+    return W, keep
 
 
 class Context:
@@ -300,6 +330,31 @@ class Context:
                        hidden_out=None):
         _check(lib().g3attn_forward_device(self._h, C.byref(weights), token, pos, logits,
                                            int(compute_logits), hidden_out))
+
+    def upload_weights(self, weights: "Weights"):
+        """weights: a Weights of HOST addresses (the gemma3_weights_t the
+        safetensors loader fills); see host_weights()."""
+        _check(lib().g3attn_upload_weights(self._h, C.byref(weights)))
+
+    def device_weights(self) -> "Weights | None":
+        p = lib().g3attn_device_weights(self._h)
+        return None if not p else Weights.from_address(p)
+
+    def forward_token(self, token, pos, compute_logits=True) -> np.ndarray | None:
+        """gemma3_metal_forward_token: logits [vocab] on the host, or None."""
+        out = np.empty(self.cfg.vocab_size, np.float32) if compute_logits else None
+        _check(lib().g3attn_forward_token(self._h, int(token), int(pos),
+                                          None if out is None else out.ctypes.data,
+                                          int(compute_logits)))
+        return out
+
+    def prefill_tokens(self, tokens, start_pos=0, logits=True) -> np.ndarray | None:
+        """gemma3_metal_prefill: the last token's logits, or None."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        out = np.empty(self.cfg.vocab_size, np.float32) if logits else None
+        _check(lib().g3attn_prefill_tokens(self._h, tokens, tokens.size, int(start_pos),
+                                           None if out is None else out.ctypes.data))
+        return out
 
     def layer_attention_device(self, layer, pos, x, wq, wk, wv, wo, q_norm, k_norm, out):
         _check(lib().g3attn_layer_attention_device(self._h, layer, pos, x, wq, wk, wv, wo, q_norm,

@@ -114,6 +114,13 @@ struct g3attn_ctx {
     /* token forward activations: x | x_norm | proj | mlp | h (see forward) */
     float *d_fw;
     size_t d_fw_cap;
+    /* uploaded model (g3attn_upload_weights): one device arena holding every
+     * tensor, the struct of device addresses into it, and the logits of the
+     * host-output forward (device, and pinned host staging) */
+    void *d_wt;
+    g3attn_weights wt;
+    int have_wt;
+    float *d_logits, *h_logits;
     /* prefill: staging sets *d_vflag = pf_epoch when a value is not exactly
      * bf16 (the attention kernel then adds its V_lo pass) */
     int *d_vflag;
@@ -165,6 +172,9 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_vflag);
     hipFree(c->d_la);
     hipFree(c->d_fw);
+    hipFree(c->d_wt);
+    hipFree(c->d_logits);
+    if (c->h_logits) hipHostFree(c->h_logits);
     if (c->h_in) hipHostFree(c->h_in);
     if (c->h_out) hipHostFree(c->h_out);
     if (c->stream) hipStreamDestroy(c->stream);
@@ -1046,6 +1056,198 @@ int g3attn_forward_device(g3attn_ctx *c, const g3attn_weights *w, int token_id, 
     if (hidden_out)
         HIP_TRY(hipMemcpyAsync(hidden_out, x, (size_t)hid * 4, hipMemcpyDeviceToDevice, c->stream),
                 "g3attn_forward_device hidden");
+    return G3_OK;
+}
+
+/* ---------------------------------------------------------- uploaded model */
+
+/* Element counts of the 13 per-layer tensors in the g3attn_layer_weights
+ * order, the sizes gemma3_metal_upload_weights wraps (gemma3_metal.m:580-594). */
+_Static_assert(sizeof(g3attn_layer_weights) == 13 * sizeof(const uint16_t *),
+               "g3attn_layer_weights is 13 tensor pointers, in order");
+static void layer_tensor_sizes(const g3attn_config *cfg, size_t n[13]) {
+    const size_t hs = (size_t)cfg->hidden_size, is = (size_t)cfg->intermediate_size;
+    const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D;
+    const size_t sz[13] = {hs, qs * hs, ks * hs, ks * hs, hs * qs, D, D, hs, is * hs, is * hs, hs * is, hs, hs};
+    memcpy(n, sz, sizeof sz);
+}
+
+/* Host -> device through two pinned 32 MiB buffers: the CPU copies chunk i+1
+ * out of the source (which may be a file mapping) while the DMA engine moves
+ * chunk i. */
+#define UP_CHUNK ((size_t)32 << 20)
+typedef struct {
+    unsigned char *stage[2];
+    hipEvent_t done[2];
+    int next;
+} uploader;
+
+static int up_copy(g3attn_ctx *c, uploader *u, void *dst, const void *src, size_t bytes) {
+    for (size_t off = 0; off < bytes; off += UP_CHUNK) {
+        const size_t n = bytes - off < UP_CHUNK ? bytes - off : UP_CHUNK;
+        const int b = u->next;
+        u->next ^= 1;
+        HIP_TRY(hipEventSynchronize(u->done[b]), "g3attn_upload_weights");
+        memcpy(u->stage[b], (const unsigned char *)src + off, n);
+        HIP_TRY(hipMemcpyAsync((unsigned char *)dst + off, u->stage[b], n, hipMemcpyHostToDevice, c->stream),
+                "g3attn_upload_weights copy");
+        HIP_TRY(hipEventRecord(u->done[b], c->stream), "g3attn_upload_weights");
+    }
+    return G3_OK;
+}
+
+int g3attn_upload_weights(g3attn_ctx *c, const void *weights) {
+    if (!c || !weights) {
+        set_err("g3attn_upload_weights: null context or weights");
+        return G3_ERR_INVALID_ARG;
+    }
+    const g3attn_weights *w = (const g3attn_weights *)weights;
+    const g3attn_config *cfg = &c->cfg;
+    const int L = cfg->num_layers;
+    if (L > G3ATTN_MAX_LAYERS || cfg->vocab_size < 1 || cfg->hidden_size < 1 || cfg->intermediate_size < 1) {
+        set_err("g3attn_upload_weights: %d layers (max %d), vocab %d, hidden %d, intermediate %d", L,
+                G3ATTN_MAX_LAYERS, cfg->vocab_size, cfg->hidden_size, cfg->intermediate_size);
+        return G3_ERR_INVALID_ARG;
+    }
+    if (!w->embed_tokens || !w->norm) {
+        set_err("g3attn_upload_weights: embed_tokens or norm is NULL");
+        return G3_ERR_INVALID_ARG;
+    }
+    size_t n[13];
+    layer_tensor_sizes(cfg, n);
+    const size_t embed_n = (size_t)cfg->vocab_size * cfg->hidden_size, norm_n = (size_t)cfg->hidden_size;
+    size_t total = align256(embed_n * 2) + align256(norm_n * 2);
+    for (int l = 0; l < L; l++) {
+        const uint16_t *t[13];
+        memcpy(t, &w->layers[l], sizeof t);
+        for (int j = 0; j < 13; j++)
+            if (t[j]) total += align256(n[j] * 2);
+    }
+    hipSetDevice(c->device);
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_upload_weights");
+    hipFree(c->d_wt);
+    c->d_wt = NULL;
+    c->have_wt = 0;
+    memset(&c->wt, 0, sizeof c->wt);
+    if (!alloc_dev(&c->d_wt, total, "weights")) return G3_ERR_OUT_OF_MEMORY;
+
+    uploader u;
+    memset(&u, 0, sizeof u);
+    int rc = G3_OK;
+    for (int b = 0; b < 2 && !rc; b++) {
+        if (hipHostMalloc((void **)&u.stage[b], UP_CHUNK, 0) != hipSuccess || hipEventCreate(&u.done[b]) != hipSuccess) {
+            set_err("g3attn_upload_weights: pinned staging allocation failed");
+            rc = G3_ERR_OUT_OF_MEMORY;
+        }
+    }
+    g3attn_weights dw;
+    memset(&dw, 0, sizeof dw);
+    unsigned char *p = (unsigned char *)c->d_wt;
+    if (!rc) {
+        dw.embed_tokens = (const uint16_t *)p;
+        rc = up_copy(c, &u, p, w->embed_tokens, embed_n * 2);
+        p += align256(embed_n * 2);
+    }
+    if (!rc) {
+        dw.norm = (const uint16_t *)p;
+        rc = up_copy(c, &u, p, w->norm, norm_n * 2);
+        p += align256(norm_n * 2);
+    }
+    for (int l = 0; l < L && !rc; l++) {
+        const uint16_t *src[13], *dst[13] = {NULL};
+        memcpy(src, &w->layers[l], sizeof src);
+        for (int j = 0; j < 13 && !rc; j++) {
+            if (!src[j]) continue;   /* optional norms stay NULL, as on the host */
+            dst[j] = (const uint16_t *)p;
+            rc = up_copy(c, &u, p, src[j], n[j] * 2);
+            p += align256(n[j] * 2);
+        }
+        memcpy(&dw.layers[l], dst, sizeof dst);
+    }
+    if (hipStreamSynchronize(c->stream) != hipSuccess && !rc) rc = hip_fail(hipGetLastError(), "g3attn_upload_weights");
+    for (int b = 0; b < 2; b++) {
+        if (u.stage[b]) hipHostFree(u.stage[b]);
+        if (u.done[b]) hipEventDestroy(u.done[b]);
+    }
+    if (rc) {
+        hipFree(c->d_wt);
+        c->d_wt = NULL;
+        return rc;
+    }
+    c->wt = dw;
+    c->have_wt = 1;
+    return G3_OK;
+}
+
+const g3attn_weights *g3attn_device_weights(g3attn_ctx *c) { return c && c->have_wt ? &c->wt : NULL; }
+
+/* Enqueue one token on the uploaded model; when want_logits, its logits land
+ * in c->d_logits. */
+static int forward_uploaded(g3attn_ctx *c, int token_id, int pos, int want_logits, const char *who) {
+    if (!c->have_wt) {
+        set_err("%s: no weights uploaded (g3attn_upload_weights)", who);
+        return G3_ERR_INVALID_ARG;
+    }
+    if (want_logits && !c->d_logits) {
+        const size_t vb = (size_t)c->cfg.vocab_size * sizeof(float);
+        if (!alloc_dev((void **)&c->d_logits, vb, "logits")) return G3_ERR_OUT_OF_MEMORY;
+        if (hipHostMalloc((void **)&c->h_logits, vb, 0) != hipSuccess) {
+            c->h_logits = NULL;
+            set_err("%s: pinned logits allocation failed", who);
+            return G3_ERR_OUT_OF_MEMORY;
+        }
+    }
+    return g3attn_forward_device(c, &c->wt, token_id, pos, want_logits ? c->d_logits : NULL, want_logits, NULL);
+}
+
+static int logits_to_host(g3attn_ctx *c, float *logits, const char *who) {
+    const size_t vb = (size_t)c->cfg.vocab_size * sizeof(float);
+    HIP_TRY(hipMemcpyAsync(c->h_logits, c->d_logits, vb, hipMemcpyDeviceToHost, c->stream), who);
+    HIP_TRY(hipStreamSynchronize(c->stream), who);
+    memcpy(logits, c->h_logits, vb);
+    return G3_OK;
+}
+
+int g3attn_forward_token(g3attn_ctx *c, int token_id, int pos, float *logits, int compute_logits) {
+    if (!c) {
+        set_err("g3attn_forward_token: null context");
+        return G3_ERR_INVALID_ARG;
+    }
+    hipSetDevice(c->device);
+    const int want = compute_logits && logits;
+    int rc = forward_uploaded(c, token_id, pos, want, "g3attn_forward_token");
+    if (rc) return rc;
+    if (want) return logits_to_host(c, logits, "g3attn_forward_token");
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_forward_token");
+    return G3_OK;
+}
+
+int g3attn_prefill_tokens(g3attn_ctx *c, const int *tokens, int num_tokens, int start_pos, float *logits) {
+    if (!c || !tokens || num_tokens < 1 || start_pos < 0) {
+        set_err("g3attn_prefill_tokens: null context / tokens, num_tokens < 1 or start_pos < 0");
+        return G3_ERR_INVALID_ARG;
+    }
+    if ((long long)start_pos + num_tokens > c->max_context) {
+        set_err("g3attn_prefill_tokens: positions %d..%d exceed max_context %d", start_pos,
+                start_pos + num_tokens - 1, c->max_context);
+        return G3_ERR_CONTEXT_OVERFLOW;
+    }
+    for (int i = 0; i < num_tokens; i++)
+        if (tokens[i] < 0 || tokens[i] >= c->cfg.vocab_size) {
+            set_err("g3attn_prefill_tokens: token %d at %d outside the vocabulary (%d)", tokens[i], i,
+                    c->cfg.vocab_size);
+            return G3_ERR_INVALID_ARG;
+        }
+    hipSetDevice(c->device);
+    /* every token is enqueued without a host round trip; only the last one
+     * computes logits (gemma3_metal.m:977-987) */
+    for (int i = 0; i < num_tokens; i++) {
+        const int last = i == num_tokens - 1;
+        const int rc = forward_uploaded(c, tokens[i], start_pos + i, last && logits, "g3attn_prefill_tokens");
+        if (rc) return rc;
+    }
+    if (logits) return logits_to_host(c, logits, "g3attn_prefill_tokens");
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_prefill_tokens");
     return G3_OK;
 }
 

@@ -219,6 +219,36 @@ typedef struct {
 int g3attn_forward_device(g3attn_ctx *ctx, const g3attn_weights *weights, int token_id, int pos,
                           float *logits, int compute_logits, float *hidden_out);
 
+/* The model on the device, the GPU side of the reference's backend hook
+ * (the USE_MPS precedent: gemma3_transformer.c:17-31, 889-905, 931-935,
+ * 954-958, 974-978).
+ *
+ * g3attn_upload_weights replaces gemma3_metal_upload_weights
+ * (gemma3_metal.m:560-601): weights points at the host gemma3_weights_t
+ * (gemma3_transformer.c:55-73, the layout of g3attn_weights), typically the
+ * safetensors mmap (gemma3_safetensors.c:651-712).  Every tensor is copied,
+ * sized from the context's config, into one device allocation through pinned
+ * staging buffers; NULL optional norms stay NULL.  A second call replaces the
+ * model.  Returns 0, -1 (missing embed_tokens / norm, bad config) or -4. */
+int g3attn_upload_weights(g3attn_ctx *ctx, const void *weights);
+
+/* The device addresses of the uploaded model, NULL before an upload (for
+ * g3attn_forward_device callers that keep their own activations). */
+const g3attn_weights *g3attn_device_weights(g3attn_ctx *ctx);
+
+/* gemma3_metal_forward_token (gemma3_metal.m:620-971), the body of
+ * gemma3_transformer_forward_token's backend branch (gemma3_transformer.c:
+ * 930-935): one token on the uploaded model; logits [vocab_size] is host
+ * memory, written when compute_logits and logits are set.  Blocking. */
+int g3attn_forward_token(g3attn_ctx *ctx, int token_id, int pos, float *logits, int compute_logits);
+
+/* gemma3_metal_prefill (gemma3_metal.m:977-987), gemma3_transformer_
+ * prefill_tokens' backend branch (:953-958): tokens[0..n-1] at positions
+ * start_pos.. through the uploaded model, enqueued back to back; logits (host,
+ * may be NULL) receives the last token's logits.  Tokens and positions are
+ * checked before anything is enqueued.  Blocking. */
+int g3attn_prefill_tokens(g3attn_ctx *ctx, const int *tokens, int num_tokens, int start_pos, float *logits);
+
 /* The context's HIP stream (hipStream_t), for callers that interleave their
  * own work; and a wait for everything queued on it. */
 void *g3attn_stream(g3attn_ctx *ctx);

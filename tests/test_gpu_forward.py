@@ -120,3 +120,108 @@ def test_forward_argument_errors():
         W.layers[2].q_proj = q
         ctx.forward_device(W, 1, 0, dl.ptr)
         assert np.all(np.isfinite(dl.download(np.float32, f["vocab"])))
+
+
+# ---------------------------------------------------------------- uploaded model
+# g3attn_upload_weights / g3attn_forward_token / g3attn_prefill_tokens: the
+# backend hook's calls (gemma3_metal_upload_weights, _forward_token, _prefill;
+# gemma3_metal.m:560-601, 620-971, 977-987).
+
+def test_upload_and_forward_token_match_reference_golden():
+    """Host weights -> upload -> forward_token (host logits) reproduces the
+    reference's logits, and equals forward_device on the same device copies
+    bit for bit (same kernels, same order)."""
+    g = np.load(os.path.join(GOLD, "forward.npz"), allow_pickle=False)
+    cfg, f, embed, layers, norm, tokens = MG.forward_case()
+    HW, keep = G.host_weights(embed, layers, norm)
+    with G.Context(_gpu_config(f), f["max_context"]) as ctx:
+        assert ctx.device_weights() is None
+        ctx.upload_weights(HW)
+        rows = [ctx.forward_token(int(t), i) for i, t in enumerate(tokens)]
+        DW = ctx.device_weights()
+        assert DW is not None and DW.layers[3].q_norm is None and DW.layers[2].q_norm is not None
+    logits = np.stack(rows)
+    err = rel_err(logits[list(g["rows"])], g["logits"])
+    print(f"[forward_token golden] rel={err:.3e}", flush=True)
+    assert err < 1e-4
+    assert np.array_equal(logits.argmax(axis=1), g["argmax"])
+    with G.Context(_gpu_config(f), f["max_context"]) as ctx:
+        W, bufs = _upload(embed, layers, norm)
+        dev_rows, _ = _run(ctx, W, tokens, f)
+    assert np.array_equal(logits, np.stack(dev_rows))
+
+
+def test_upload_from_a_file_mapping(tmp_path):
+    """The loader's case: tensors packed in one mapped file at 2-byte-aligned
+    offsets (as in a safetensors blob), uploaded straight from the mapping."""
+    g = np.load(os.path.join(GOLD, "forward.npz"), allow_pickle=False)
+    cfg, f, embed, layers, norm, tokens = MG.forward_case()
+    arrays = [embed, norm] + [lw[n] for lw in layers for n in G.LAYER_TENSORS if lw[n] is not None]
+    path = tmp_path / "weights.bin"
+    offs, off = [], 2                       # start 2 bytes in: nothing is 16-byte aligned by luck
+    with open(path, "wb") as fh:
+        fh.write(b"\0\0")
+        for a in arrays:
+            offs.append(off)
+            fh.write(np.ascontiguousarray(a, np.uint16).tobytes())
+            off += a.nbytes + 2
+            fh.write(b"\0\0")
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    views = iter([mm[o:o + a.nbytes].view(np.uint16) for o, a in zip(offs, arrays)])
+    HW = G.Weights()
+    HW.embed_tokens, HW.norm = next(views).ctypes.data, next(views).ctypes.data
+    for l, lw in enumerate(layers):
+        for n in G.LAYER_TENSORS:
+            if lw[n] is not None:
+                setattr(HW.layers[l], n, next(views).ctypes.data)
+    assert HW.embed_tokens % 16 == 2
+    with G.Context(_gpu_config(f), f["max_context"]) as ctx:
+        ctx.upload_weights(HW)
+        del mm
+        last = None
+        for i, t in enumerate(tokens):
+            last = ctx.forward_token(int(t), i, compute_logits=(i == len(tokens) - 1))
+    print("[upload mmap] ok", flush=True)
+    assert rel_err(last, g["logits"][-1]) < 1e-4
+
+
+def test_prefill_tokens_equals_the_token_loop():
+    """prefill_tokens enqueues the tokens back to back and returns the last
+    token's logits: bit-identical to forward_token one by one, and decoding
+    continues from it identically."""
+    cfg, f, embed, layers, norm, tokens = MG.forward_case()
+    HW, keep = G.host_weights(embed, layers, norm)
+    n = 25
+    with G.Context(_gpu_config(f), f["max_context"]) as a, G.Context(_gpu_config(f), f["max_context"]) as b:
+        a.upload_weights(HW)
+        b.upload_weights(HW)
+        want = [a.forward_token(int(t), i) for i, t in enumerate(tokens[:n + 3])]
+        got = b.prefill_tokens(tokens[:n])
+        assert np.array_equal(got, want[n - 1])
+        assert b.prefill_tokens(tokens[n:n + 2], start_pos=n, logits=False) is None
+        assert np.array_equal(b.forward_token(int(tokens[n + 2]), n + 2), want[n + 2])
+    print("[prefill_tokens] ok", flush=True)
+
+
+def test_uploaded_model_errors():
+    cfg, f, embed, layers, norm, tokens = MG.forward_case(n=4)
+    with G.Context(_gpu_config(f), f["max_context"]) as ctx:
+        with pytest.raises(G.G3AttnError):
+            ctx.forward_token(1, 0)                              # nothing uploaded
+        HW, keep = G.host_weights(embed, layers, None)
+        with pytest.raises(G.G3AttnError):
+            ctx.upload_weights(HW)                               # no final norm
+        HW, keep = G.host_weights(embed, layers, norm)
+        ctx.upload_weights(HW)
+        with pytest.raises(G.G3AttnError):
+            ctx.prefill_tokens([1, 2, f["vocab"], 3])            # checked before any work
+        with pytest.raises(G.G3AttnError) as e:
+            ctx.prefill_tokens([1] * 5, start_pos=f["max_context"] - 4)
+        assert e.value.rc == G.ERR_CONTEXT_OVERFLOW
+        first = ctx.forward_token(int(tokens[0]), 0)
+        # a second upload replaces the model
+        other = [dict(lw) for lw in layers]
+        other[0]["down_proj"] = MG.weights_bf16(f["hidden"], f["inter"], 0xD0D0)
+        HW2, keep2 = G.host_weights(embed, other, norm)
+        ctx.upload_weights(HW2)
+        assert not np.array_equal(ctx.forward_token(int(tokens[0]), 0), first)

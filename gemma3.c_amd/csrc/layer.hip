@@ -55,10 +55,21 @@ __global__ __launch_bounds__(NT) void embed_kernel(g3k_layer_args a) {
     for (int i = threadIdx.x; i < n; i += NT) a.x[i] = bf16f(row[i]) * scale;
 }
 
+// The gains (1 + w) of a norm, loaded up front so that their latency overlaps
+// the activations' loads instead of following a reduction.
+__device__ __forceinline__ void load_gain(float (&g)[PER], const uint16_t *w, int n) {
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + NT * u;
+        g[u] = (w && i < n) ? 1.0f + bf16f(w[i]) : 0.f;
+    }
+}
+
 __global__ __launch_bounds__(NT) void norm_kernel(g3k_layer_args a) {
     __shared__ float red[NW];
     const int n = a.n;
-    float v[PER];
+    float v[PER], g[PER];
+    load_gain(g, a.w_next, n);
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const int i = threadIdx.x + NT * u;
@@ -68,14 +79,16 @@ __global__ __launch_bounds__(NT) void norm_kernel(g3k_layer_args a) {
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const int i = threadIdx.x + NT * u;
-        if (i < n) a.y[i] = v[u] * r * (1.0f + bf16f(a.w_next[i]));
+        if (i < n) a.y[i] = v[u] * r * g[u];
     }
 }
 
 __global__ __launch_bounds__(NT) void residual_kernel(g3k_layer_args a) {
     __shared__ float red[NW];
     const int n = a.n;
-    float t[PER], x[PER];
+    float t[PER], x[PER], gp[PER], gn[PER];
+    load_gain(gp, a.w_post, n);
+    load_gain(gn, a.y ? a.w_next : nullptr, n);
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const int i = threadIdx.x + NT * u;
@@ -85,10 +98,7 @@ __global__ __launch_bounds__(NT) void residual_kernel(g3k_layer_args a) {
     if (a.w_post) {
         const float r = rms_scale(t, n, a.eps, red);
 #pragma unroll
-        for (int u = 0; u < PER; u++) {
-            const int i = threadIdx.x + NT * u;
-            t[u] = i < n ? t[u] * r * (1.0f + bf16f(a.w_post[i])) : 0.f;
-        }
+        for (int u = 0; u < PER; u++) t[u] = t[u] * r * gp[u];   // gp is 0 past n
     }
 #pragma unroll
     for (int u = 0; u < PER; u++) {
@@ -102,7 +112,7 @@ __global__ __launch_bounds__(NT) void residual_kernel(g3k_layer_args a) {
 #pragma unroll
         for (int u = 0; u < PER; u++) {
             const int i = threadIdx.x + NT * u;
-            if (i < n) a.y[i] = x[u] * r * (1.0f + bf16f(a.w_next[i]));
+            if (i < n) a.y[i] = x[u] * r * gn[u];
         }
     } else {
 #pragma unroll

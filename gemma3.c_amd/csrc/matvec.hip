@@ -10,12 +10,18 @@
 //
 // At decode batch 1 the GEMV is HBM-bound: 2 bytes of A per multiply-add.
 // Workgroup = 4 waves; each wave owns RPW consecutive rows.  Lane l reads the
-// 16-byte chunks 8 l + 512 j of each row, so one wave load covers 1 KiB of a
-// row, contiguous, and all of a row's loads (rows up to 4096 elements; longer
-// rows in rounds of that size) are issued, with the x chunks they meet, before
-// the FMAs that use them.  x is small and read through the caches.  Row sums
-// reduce over the wave with DPP and permlane swaps.  Rows whose length is not
-// a multiple of 8 (or unaligned buffers) take a lane-strided scalar path.
+// 16-byte chunks l + 64 j of each row (8 elements each), so one wave load
+// covers 1 KiB of a row, contiguous; CH chunks per lane (a round) are issued,
+// with the x chunks they meet, before the FMAs that use them.  A is streamed
+// with non-temporal loads: every byte is read once, and keeping it out of the
+// caches leaves them to x.  Row sums reduce over the wave with DPP and
+// permlane swaps.  Rows whose length is not a multiple of 8 (or unaligned
+// buffers) take a lane-strided scalar path.
+//
+// Shapes pick the variant (measured on the forward's shapes): long rows
+// (K >= 8192, the MLP's down projection) stage x in LDS once per workgroup
+// instead of once per wave; rows of at most 2048 elements take 4 chunks per
+// round (one round); very tall matrices (the tied logits) take 2 rows per wave.
 //
 // One launch can serve up to three matrices that share x (the Q, K and V
 // projections of one token): workgroups are dealt to the matrices in order of
@@ -32,6 +38,7 @@ using namespace g3k;
 
 constexpr int NT = 256;   // 4 waves
 constexpr int NW = NT / 64;
+constexpr int G3K_MATVEC_LDS_MAX_K = 16384;
 
 __device__ __forceinline__ float dot8(uint4 w, float4 xa, float4 xb) {
     float s = bf16f(w.x & 0xffff) * xa.x;
@@ -68,10 +75,21 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes of A, non-temporal (read once).
+__device__ __forceinline__ uint4 load_a(const uint16_t *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // NA dot products per wave: RPW consecutive rows of one matrix, or (GEGLU)
-// the same row of the gate and up matrices.
-template <int RPW, bool VEC, bool GEGLU>
+// the same row of the gate and up matrices.  XLDS: x is copied to LDS by the
+// workgroup (dynamic shared memory of K floats) after the first round's A
+// loads are issued.
+template <int RPW, int CH, bool VEC, bool XLDS, bool GEGLU>
 __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
+    extern __shared__ float4 xs4[];
     constexpr int NA = GEGLU ? 2 : RPW;
     const int K = a.K;
     int row0;
@@ -92,28 +110,38 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
     for (int j = 0; j < NA; j++) acc[j] = 0.f;
 
     if (VEC) {
-        // 16-byte chunks: chunk c covers elements 8c .. 8c + 7; lane l takes
-        // chunks l, l + 64, ...  All CH chunks of a round (a whole row of up
-        // to 4096 elements) are requested, with their x, before any FMA.
-        constexpr int CH = GEGLU ? 4 : 8;
         const int nch = K >> 3;
-        for (int c0 = lane; c0 < nch; c0 += 64 * CH) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        // rounds are uniform over the workgroup (the LDS copy has a barrier)
+        for (int base = 0; base < nch; base += 64 * CH) {
             uint4 w[NA][CH];
             float4 xa[CH], xb[CH];
 #pragma unroll
             for (int u = 0; u < CH; u++) {
-                const int c = c0 + 64 * u;
+                const int c = base + lane + 64 * u;
                 const bool ok = c < nch;
 #pragma unroll
-                for (int j = 0; j < NA; j++)
-                    w[j][u] = ok ? *reinterpret_cast<const uint4 *>(rows[j] + 8 * c) : make_uint4(0, 0, 0, 0);
-                xa[u] = ok ? *reinterpret_cast<const float4 *>(x + 8 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-                xb[u] = ok ? *reinterpret_cast<const float4 *>(x + 8 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int j = 0; j < NA; j++) w[j][u] = ok ? load_a(rows[j] + 8 * c) : make_uint4(0, 0, 0, 0);
+                if (!XLDS) {
+                    xa[u] = ok ? x4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    xb[u] = ok ? x4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+            if (XLDS && base == 0) {
+                for (int i = threadIdx.x; i < 2 * nch; i += NT) xs4[i] = x4[i];
+                __syncthreads();
             }
 #pragma unroll
-            for (int u = 0; u < CH; u++)
+            for (int u = 0; u < CH; u++) {
+                if (XLDS) {
+                    const int c = base + lane + 64 * u;
+                    const bool ok = c < nch;
+                    xa[u] = ok ? xs4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    xb[u] = ok ? xs4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
 #pragma unroll
                 for (int j = 0; j < NA; j++) acc[j] += dot8(w[j][u], xa[u], xb[u]);
+            }
         }
     } else {
         for (int k = lane; k < K; k += 64) {
@@ -134,12 +162,13 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
     }
 }
 
-template <int RPW, bool VEC, bool GEGLU = false>
+template <int RPW, int CH, bool VEC, bool XLDS = false, bool GEGLU = false>
 hipError_t launch(const g3k_matvec_args *a, hipStream_t st) {
     int blocks = 0;
     const int nm = GEGLU ? 1 : a->n_mat;
     for (int m = 0; m < nm; m++) blocks += (a->M[m] + NW * RPW - 1) / (NW * RPW);
-    hipLaunchKernelGGL((matvec_kernel<RPW, VEC, GEGLU>), dim3(blocks), dim3(NT), 0, st, *a);
+    const size_t lds = XLDS ? (size_t)a->K * sizeof(float) : 0;
+    hipLaunchKernelGGL((matvec_kernel<RPW, CH, VEC, XLDS, GEGLU>), dim3(blocks), dim3(NT), lds, st, *a);
     return hipGetLastError();
 }
 
@@ -161,10 +190,14 @@ extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (a->mode == G3K_MV_GEGLU) {
         if (a->n_mat != 2 || a->M[0] != a->M[1]) return (int)hipErrorInvalidValue;
-        return (int)(vec ? launch<1, true, true>(a, st) : launch<1, false, true>(a, st));
+        return (int)(vec ? launch<1, 4, true, false, true>(a, st) : launch<1, 1, false, false, true>(a, st));
     }
     if (a->mode != 0) return (int)hipErrorInvalidValue;
+    if (!vec) return (int)(rows >= 16384 ? launch<2, 1, false>(a, st) : launch<1, 1, false>(a, st));
     // two rows per wave once there are enough rows to fill the chip with them
-    if (rows >= 16384) return (int)(vec ? launch<2, true>(a, st) : launch<2, false>(a, st));
-    return (int)(vec ? launch<1, true>(a, st) : launch<1, false>(a, st));
+    if (rows >= 16384) return (int)launch<2, 8, true>(a, st);
+    // long rows: x in LDS (K floats, at most 64 KiB of the workgroup's LDS)
+    if (a->K >= 8192 && a->K <= G3K_MATVEC_LDS_MAX_K) return (int)launch<1, 4, true, true>(a, st);
+    if (a->K <= 2048) return (int)launch<1, 4, true>(a, st);
+    return (int)launch<1, 8, true>(a, st);
 }

@@ -48,10 +48,13 @@ def test_matvec_matches_reference_golden(name):
 
 
 @pytest.mark.parametrize("M,K", [(1, 1), (3, 7), (64, 8), (65, 16), (37, 1000), (5, 2565),
-                                 (300, 4096), (2560, 10240), (20000, 512)])
+                                 (9, 2048), (300, 4096), (2560, 10240), (7, 8200), (3, 16392),
+                                 (20000, 512), (16385, 2560)])
 def test_matvec_shapes(M, K):
     """Vector path (K % 8 == 0), scalar path (ragged K), one and two rows per
-    wave (the launch switches at 16384 rows), long rows (x in LDS)."""
+    wave (the launch switches at 16384 rows), one round of 4 chunks (K <=
+    2048), long rows with x in LDS (8192 <= K <= 16384, here with a partial
+    last round) and past the LDS limit."""
     rng = np.random.default_rng(M * 131 + K)
     A = MG.weights_bf16(M, K, 0xA000 + M + K)
     x = rng.standard_normal(K).astype(np.float32)

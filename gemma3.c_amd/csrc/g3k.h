@@ -177,6 +177,50 @@ typedef struct {
 
 int g3k_layer_step(const g3k_layer_args *a, void *stream);
 
+/* The same steps over `rows` tokens at once, one workgroup per token row, for
+ * the batched prefill.  The normed output goes to two bf16 planes, y = y_hi +
+ * y_lo (y_hi = bf16(y), y_lo = bf16(y - y_hi)), the GEMM operand format:
+ *   G3K_ROWS_EMBED:    x[r] = bf16(embed[tokens[r]][.]) * sqrt(n);
+ *                      y[r] = rmsnorm(x[r], w_next)
+ *   G3K_ROWS_RESIDUAL: t' = rmsnorm(t[r], w_post) if w_post, else t[r];
+ *                      x[r] += t'; then, if y_hi: y[r] = rmsnorm(x[r], w_next),
+ *                      or x[r] itself if w_next is NULL
+ *   G3K_ROWS_SPLIT:    y[r] = t[r] (any n; the other ops take n <= G3K_LAYER_MAX_HIDDEN)
+ * x is [rows][n] fp32, t [rows][ldt] fp32, y_hi / y_lo [rows][ldy] bf16;
+ * tokens is a device array. */
+enum { G3K_ROWS_EMBED = 0, G3K_ROWS_RESIDUAL = 1, G3K_ROWS_SPLIT = 2 };
+typedef struct {
+    int op, rows, n;
+    float eps;
+    const int *tokens;
+    const uint16_t *embed, *w_post, *w_next;
+    float *x;
+    const float *t;
+    int ldt;
+    uint16_t *y_hi, *y_lo;
+    int ldy;
+} g3k_rows_args;
+
+int g3k_rows(const g3k_rows_args *a, void *stream);
+
+/* Batched projection on MFMA: C[n][m] = sum_k X[n][k] W[m][k] for N tokens,
+ * X given as bf16 planes x_hi + x_lo [N][ldx], W bf16 [M][K] (K % 32 == 0,
+ * M % 4 == 0).  mode 0: n_mat (1..3) matrices sharing X, each written to
+ * C[j] [N][ldc[j]] fp32.  mode G3K_MV_GEGLU: W[0] = gate, W[1] = up (same M);
+ * gelu_tanh(gate) * up is written as bf16 planes h_hi + h_lo [N][ldh]. */
+typedef struct {
+    const uint16_t *x_hi, *x_lo;
+    int N, K, ldx, n_mat, mode;
+    const uint16_t *W[G3K_MATVEC_MAX];
+    int M[G3K_MATVEC_MAX];
+    float *C[G3K_MATVEC_MAX];
+    int ldc[G3K_MATVEC_MAX];
+    uint16_t *h_hi, *h_lo;
+    int ldh;
+} g3k_gemm_args;
+
+int g3k_gemm(const g3k_gemm_args *a, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

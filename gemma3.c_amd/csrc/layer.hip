@@ -146,3 +146,134 @@ extern "C" int g3k_layer_step(const g3k_layer_args *a, void *stream) {
     }
     return (int)hipGetLastError();
 }
+
+// ------------------------------------------------------------ batched rows
+// One workgroup of 256 threads per token row (gemma3_transformer.c:585-592,
+// 596-602, 702-724, 753-765: the reference's per-token loops of the batched
+// prefill).  Values per thread: n <= 256 * RPER.
+
+namespace {
+
+constexpr int RNT = 256;
+constexpr int RNW = RNT / 64;
+constexpr int RPER = G3K_LAYER_MAX_HIDDEN / RNT;
+
+__device__ __forceinline__ float rblock_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < RNW; w++) s += red[w];
+    return s;
+}
+
+__device__ __forceinline__ uint32_t rne16(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// y = v * r * gain (gain 1 where w is NULL) as bf16 hi / lo planes
+__device__ __forceinline__ void store_split(const g3k_rows_args &a, int row, const float (&v)[RPER], float r,
+                                            const uint16_t *w) {
+    uint16_t *yh = a.y_hi + (size_t)row * a.ldy, *yl = a.y_lo + (size_t)row * a.ldy;
+#pragma unroll
+    for (int u = 0; u < RPER; u++) {
+        const int i = threadIdx.x + RNT * u;
+        if (i < a.n) {
+            const float y = w ? v[u] * r * (1.0f + bf16f(w[i])) : v[u];
+            const uint32_t hi = rne16(y);
+            yh[i] = (uint16_t)hi;
+            yl[i] = (uint16_t)rne16(y - __uint_as_float(hi << 16));
+        }
+    }
+}
+
+__global__ __launch_bounds__(RNT) void rows_kernel(g3k_rows_args a) {
+    __shared__ float red[RNW];
+    const int row = blockIdx.x, n = a.n;
+    float v[RPER];
+    if (a.op == G3K_ROWS_SPLIT) {   // elementwise: any row length
+        const float *t = a.t + (size_t)row * a.ldt;
+        uint16_t *yh = a.y_hi + (size_t)row * a.ldy, *yl = a.y_lo + (size_t)row * a.ldy;
+        for (int i = threadIdx.x; i < n; i += RNT) {
+            const float y = t[i];
+            const uint32_t hi = rne16(y);
+            yh[i] = (uint16_t)hi;
+            yl[i] = (uint16_t)rne16(y - __uint_as_float(hi << 16));
+        }
+        return;
+    }
+    float *x = a.x + (size_t)row * n;
+    if (a.op == G3K_ROWS_EMBED) {
+        const float scale = sqrtf((float)n);
+        const uint16_t *e = a.embed + (size_t)a.tokens[row] * n;
+#pragma unroll
+        for (int u = 0; u < RPER; u++) {
+            const int i = threadIdx.x + RNT * u;
+            v[u] = i < n ? bf16f(e[i]) * scale : 0.f;
+            if (i < n) x[i] = v[u];
+        }
+    } else {
+        const float *t = a.t + (size_t)row * a.ldt;
+        float tv[RPER];
+#pragma unroll
+        for (int u = 0; u < RPER; u++) {
+            const int i = threadIdx.x + RNT * u;
+            tv[u] = i < n ? t[i] : 0.f;
+            v[u] = i < n ? x[i] : 0.f;
+        }
+        if (a.w_post) {
+            float ss = 0.f;
+#pragma unroll
+            for (int u = 0; u < RPER; u++) ss += tv[u] * tv[u];
+            const float r = 1.0f / sqrtf(rblock_sum(ss, red) / (float)n + a.eps);
+#pragma unroll
+            for (int u = 0; u < RPER; u++) {
+                const int i = threadIdx.x + RNT * u;
+                tv[u] = i < n ? tv[u] * r * (1.0f + bf16f(a.w_post[i])) : 0.f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < RPER; u++) {
+            const int i = threadIdx.x + RNT * u;
+            v[u] = v[u] + tv[u];
+            if (i < n) x[i] = v[u];
+        }
+        if (!a.y_hi) return;   // uniform
+    }
+    float r = 1.f;
+    if (a.w_next) {
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < RPER; u++) ss += v[u] * v[u];
+        r = 1.0f / sqrtf(rblock_sum(ss, red) / (float)n + a.eps);
+    }
+    store_split(a, row, v, r, a.w_next);
+}
+
+}  // namespace
+
+extern "C" int g3k_rows(const g3k_rows_args *a, void *stream) {
+    if (a->rows < 1 || a->n < 1 || (a->op != G3K_ROWS_SPLIT && a->n > G3K_LAYER_MAX_HIDDEN))
+        return (int)hipErrorInvalidValue;
+    const bool split_out = a->y_hi && a->y_lo && a->ldy >= a->n;
+    switch (a->op) {
+        case G3K_ROWS_EMBED:
+            if (!a->tokens || !a->embed || !a->x || !split_out) return (int)hipErrorInvalidValue;
+            break;
+        case G3K_ROWS_RESIDUAL:
+            if (!a->x || !a->t || a->ldt < a->n || ((a->y_hi || a->y_lo) && !split_out))
+                return (int)hipErrorInvalidValue;
+            break;
+        case G3K_ROWS_SPLIT:
+            if (!a->t || a->ldt < a->n || !split_out) return (int)hipErrorInvalidValue;
+            break;
+        default:
+            return (int)hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(rows_kernel, dim3(a->rows), dim3(RNT), 0, (hipStream_t)stream, *a);
+    return (int)hipGetLastError();
+}

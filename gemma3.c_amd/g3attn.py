@@ -106,13 +106,16 @@ def lib():
     L.g3attn_device_weights.restype = C.c_void_p
     L.g3attn_forward_token.argtypes = [_vp, C.c_int, C.c_int, C.c_void_p, C.c_int]
     L.g3attn_prefill_tokens.argtypes = [_vp, _i32p, C.c_int, C.c_int, C.c_void_p]
+    L.g3attn_matmul_bf16_device.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]
+    L.g3attn_prefill_forward_device.argtypes = [_vp, C.c_void_p, _i32p, C.c_int, C.c_int, _vp]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
                  "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
                  "g3attn_profile_enable", "g3attn_profile_read", "g3attn_matvec_bf16_device",
                  "g3attn_qkv_proj_device", "g3attn_layer_attention_device",
                  "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
-                 "g3attn_prefill_tokens"):
+                 "g3attn_prefill_tokens", "g3attn_matmul_bf16_device",
+                 "g3attn_prefill_forward_device"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -355,6 +358,17 @@ class Context:
         _check(lib().g3attn_prefill_tokens(self._h, tokens, tokens.size, int(start_pos),
                                            None if out is None else out.ctypes.data))
         return out
+
+    def matmul_bf16_device(self, C, W, X, N, M, K):
+        """C [N][M] = X [N][K] . W [M][K]^T (device pointers)."""
+        _check(lib().g3attn_matmul_bf16_device(self._h, C, W, X, N, M, K))
+
+    def prefill_forward_device(self, weights: "Weights", tokens, start_pos=0, logits=None):
+        """The batched prefill of host tokens on device weights; logits: a
+        device address or None."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        _check(lib().g3attn_prefill_forward_device(self._h, C.byref(weights), tokens, tokens.size,
+                                                   int(start_pos), logits))
 
     def layer_attention_device(self, layer, pos, x, wq, wk, wv, wo, q_norm, k_norm, out):
         _check(lib().g3attn_layer_attention_device(self._h, layer, pos, x, wq, wk, wv, wo, q_norm,

@@ -121,6 +121,11 @@ struct g3attn_ctx {
     g3attn_weights wt;
     int have_wt;
     float *d_logits, *h_logits;
+    /* batched prefill activations (see prefill_forward) and token ids */
+    void *d_pb;
+    size_t d_pb_cap;
+    int *d_tok;
+    size_t d_tok_cap;
     /* prefill: staging sets *d_vflag = pf_epoch when a value is not exactly
      * bf16 (the attention kernel then adds its V_lo pass) */
     int *d_vflag;
@@ -174,6 +179,8 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_fw);
     hipFree(c->d_wt);
     hipFree(c->d_logits);
+    hipFree(c->d_pb);
+    hipFree(c->d_tok);
     if (c->h_logits) hipHostFree(c->h_logits);
     if (c->h_in) hipHostFree(c->h_in);
     if (c->h_out) hipHostFree(c->h_out);
@@ -1059,6 +1066,292 @@ int g3attn_forward_device(g3attn_ctx *c, const g3attn_weights *w, int token_id, 
     return G3_OK;
 }
 
+/* ---------------------------------------------------------- batched GEMM */
+
+int g3attn_matmul_bf16_device(g3attn_ctx *c, float *C, const uint16_t *W, const float *X, int N, int M, int K) {
+    if (!c || !C || !W || !X || N < 1 || M < 4 || M % 4 || K < 32 || K % 32) {
+        set_err("g3attn_matmul_bf16_device: null buffer, N < 1, M not a positive multiple of 4 or K not a "
+                "positive multiple of 32");
+        return G3_ERR_INVALID_ARG;
+    }
+    hipSetDevice(c->device);
+    const size_t plane = align256((size_t)N * K * 2);
+    int rc = grow_buf(c, (float **)&c->d_big, &c->d_big_cap, 2 * plane, "matmul planes");
+    if (rc) return rc;
+    uint16_t *xh = (uint16_t *)c->d_big, *xl = (uint16_t *)((unsigned char *)c->d_big + plane);
+    g3k_rows_args r;
+    memset(&r, 0, sizeof r);
+    r.op = G3K_ROWS_SPLIT;
+    r.rows = N;
+    r.n = K;
+    r.t = X;
+    r.ldt = K;
+    r.y_hi = xh;
+    r.y_lo = xl;
+    r.ldy = K;
+    rc = g3k_rows(&r, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_matmul_bf16_device split");
+    g3k_gemm_args g;
+    memset(&g, 0, sizeof g);
+    g.x_hi = xh;
+    g.x_lo = xl;
+    g.N = N;
+    g.K = K;
+    g.ldx = K;
+    g.n_mat = 1;
+    g.W[0] = W;
+    g.M[0] = M;
+    g.C[0] = C;
+    g.ldc[0] = M;
+    rc = g3k_gemm(&g, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_matmul_bf16_device");
+    return G3_OK;
+}
+
+/* ---------------------------------------------------------- batched prefill */
+
+/* Tokens per pass through the stack: the activations below take about 100 KiB
+ * per token at Gemma3-4B shapes (0.8 GiB at 8192). */
+#define PB_CHUNK 8192
+
+typedef struct {
+    float *x, *q, *k, *v, *attn, *t, *xn;
+    uint16_t *xh, *xl, *ah, *al, *hh, *hl;
+} pb_bufs;
+
+static int pb_layout(g3attn_ctx *c, int n, pb_bufs *b) {
+    const g3attn_config *cfg = &c->cfg;
+    const size_t hid = cfg->hidden_size, inter = cfg->intermediate_size;
+    const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D, N = n;
+    const size_t sz[13] = {N * hid * 4, N * qs * 4, N * ks * 4, N * ks * 4, N * qs * 4, N * hid * 4, hid * 4,
+                           N * hid * 2, N * hid * 2, N * qs * 2, N * qs * 2, N * inter * 2, N * inter * 2};
+    size_t total = 0;
+    for (int i = 0; i < 13; i++) total += align256(sz[i]);
+    int rc = grow_buf(c, (float **)&c->d_pb, &c->d_pb_cap, total, "prefill activations");
+    if (rc) return rc;
+    unsigned char *p = (unsigned char *)c->d_pb;
+    void **dst[13] = {(void **)&b->x, (void **)&b->q, (void **)&b->k, (void **)&b->v, (void **)&b->attn,
+                      (void **)&b->t, (void **)&b->xn, (void **)&b->xh, (void **)&b->xl, (void **)&b->ah,
+                      (void **)&b->al, (void **)&b->hh, (void **)&b->hl};
+    for (int i = 0; i < 13; i++) {
+        *dst[i] = p;
+        p += align256(sz[i]);
+    }
+    return G3_OK;
+}
+
+static int rows_step(g3attn_ctx *c, const g3k_rows_args *a) {
+    const int rc = g3k_rows(a, c->stream);
+    return rc ? hip_fail((hipError_t)rc, "g3attn_prefill_forward_device rows") : G3_OK;
+}
+
+static int gemm_step(g3attn_ctx *c, const g3k_gemm_args *a) {
+    const int rc = g3k_gemm(a, c->stream);
+    return rc ? hip_fail((hipError_t)rc, "g3attn_prefill_forward_device GEMM") : G3_OK;
+}
+
+/* One chunk of n tokens at positions pos0.. through every layer: the
+ * reference's batched prefill (gemma3_transformer.c:585-766) with the
+ * projections on MFMA and the attention on the prefill kernel. */
+static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0, const pb_bufs *b) {
+    const g3attn_config *cfg = &c->cfg;
+    const int hid = cfg->hidden_size, inter = cfg->intermediate_size, L = cfg->num_layers;
+    const int qs = cfg->num_heads * D, ks = cfg->num_kv_heads * D;
+    int rc;
+    g3k_rows_args r;
+    memset(&r, 0, sizeof r);
+    r.rows = n;
+    r.n = hid;
+    r.eps = cfg->rmsnorm_eps;
+    /* embedding * sqrt(hidden) and layer 0's input norm (:585-602) */
+    r.op = G3K_ROWS_EMBED;
+    r.tokens = c->d_tok;
+    r.embed = w->embed_tokens;
+    r.w_next = w->layers[0].input_layernorm;
+    r.x = b->x;
+    r.y_hi = b->xh;
+    r.y_lo = b->xl;
+    r.ldy = hid;
+    if ((rc = rows_step(c, &r))) return rc;
+    for (int l = 0; l < L; l++) {
+        const g3attn_layer_weights *lw = &w->layers[l];
+        g3k_gemm_args g;
+        /* Q/K/V projections (:604-639) */
+        memset(&g, 0, sizeof g);
+        g.x_hi = b->xh;
+        g.x_lo = b->xl;
+        g.N = n;
+        g.K = hid;
+        g.ldx = hid;
+        g.n_mat = 3;
+        g.W[0] = lw->q_proj;
+        g.W[1] = lw->k_proj;
+        g.W[2] = lw->v_proj;
+        g.M[0] = qs;
+        g.M[1] = g.M[2] = ks;
+        g.C[0] = b->q;
+        g.C[1] = b->k;
+        g.C[2] = b->v;
+        g.ldc[0] = qs;
+        g.ldc[1] = g.ldc[2] = ks;
+        if ((rc = gemm_step(c, &g))) return rc;
+        /* QK-norm, RoPE, cache write, attention (:641-692) */
+        if ((rc = g3attn_prefill_device(c, l, pos0, n, b->q, b->k, b->v, lw->q_norm, lw->k_norm, b->attn)))
+            return rc;
+        /* o_proj (:694-699) */
+        memset(&r, 0, sizeof r);
+        r.op = G3K_ROWS_SPLIT;
+        r.rows = n;
+        r.n = qs;
+        r.t = b->attn;
+        r.ldt = qs;
+        r.y_hi = b->ah;
+        r.y_lo = b->al;
+        r.ldy = qs;
+        if ((rc = rows_step(c, &r))) return rc;
+        memset(&g, 0, sizeof g);
+        g.x_hi = b->ah;
+        g.x_lo = b->al;
+        g.N = n;
+        g.K = qs;
+        g.ldx = qs;
+        g.n_mat = 1;
+        g.W[0] = lw->o_proj;
+        g.M[0] = hid;
+        g.C[0] = b->t;
+        g.ldc[0] = hid;
+        if ((rc = gemm_step(c, &g))) return rc;
+        /* post-attention norm + residual, pre-feedforward norm (:701-724) */
+        memset(&r, 0, sizeof r);
+        r.op = G3K_ROWS_RESIDUAL;
+        r.rows = n;
+        r.n = hid;
+        r.eps = cfg->rmsnorm_eps;
+        r.w_post = lw->post_attention_layernorm;
+        r.w_next = lw->pre_feedforward_layernorm;
+        r.x = b->x;
+        r.t = b->t;
+        r.ldt = hid;
+        r.y_hi = b->xh;
+        r.y_lo = b->xl;
+        r.ldy = hid;
+        if ((rc = rows_step(c, &r))) return rc;
+        /* gate and up projections with gelu(gate) * up (:726-745) */
+        memset(&g, 0, sizeof g);
+        g.x_hi = b->xh;
+        g.x_lo = b->xl;
+        g.N = n;
+        g.K = hid;
+        g.ldx = hid;
+        g.n_mat = 2;
+        g.mode = G3K_MV_GEGLU;
+        g.W[0] = lw->gate_proj;
+        g.W[1] = lw->up_proj;
+        g.M[0] = g.M[1] = inter;
+        g.h_hi = b->hh;
+        g.h_lo = b->hl;
+        g.ldh = inter;
+        if ((rc = gemm_step(c, &g))) return rc;
+        /* down projection (:747-751) */
+        memset(&g, 0, sizeof g);
+        g.x_hi = b->hh;
+        g.x_lo = b->hl;
+        g.N = n;
+        g.K = inter;
+        g.ldx = inter;
+        g.n_mat = 1;
+        g.W[0] = lw->down_proj;
+        g.M[0] = hid;
+        g.C[0] = b->t;
+        g.ldc[0] = hid;
+        if ((rc = gemm_step(c, &g))) return rc;
+        /* post-feedforward norm + residual (:753-765), then the next layer's input norm */
+        const int last = l + 1 == L;
+        memset(&r, 0, sizeof r);
+        r.op = G3K_ROWS_RESIDUAL;
+        r.rows = n;
+        r.n = hid;
+        r.eps = cfg->rmsnorm_eps;
+        r.w_post = lw->post_feedforward_layernorm;
+        r.w_next = last ? NULL : w->layers[l + 1].input_layernorm;
+        r.x = b->x;
+        r.t = b->t;
+        r.ldt = hid;
+        r.y_hi = last ? NULL : b->xh;
+        r.y_lo = last ? NULL : b->xl;
+        r.ldy = hid;
+        if ((rc = rows_step(c, &r))) return rc;
+    }
+    return G3_OK;
+}
+
+int g3attn_prefill_forward_device(g3attn_ctx *c, const g3attn_weights *w, const int *tokens, int num_tokens,
+                                  int start_pos, float *logits) {
+    if (!c || !w || !tokens || num_tokens < 1 || start_pos < 0 || !w->embed_tokens || (logits && !w->norm)) {
+        set_err("g3attn_prefill_forward_device: null context / weights / tokens, num_tokens < 1 or "
+                "start_pos < 0");
+        return G3_ERR_INVALID_ARG;
+    }
+    const g3attn_config *cfg = &c->cfg;
+    const int hid = cfg->hidden_size, inter = cfg->intermediate_size, L = cfg->num_layers;
+    const int qs = cfg->num_heads * D;
+    if (L < 1 || L > G3ATTN_MAX_LAYERS || hid < 32 || hid > G3K_LAYER_MAX_HIDDEN || hid % 32 || inter < 32 ||
+        inter % 32 || qs > G3K_LAYER_MAX_HIDDEN) {
+        set_err("g3attn_prefill_forward_device: layers %d, hidden %d, intermediate %d unsupported (hidden and "
+                "intermediate must be multiples of 32, hidden <= %d)", L, hid, inter, G3K_LAYER_MAX_HIDDEN);
+        return G3_ERR_INVALID_ARG;
+    }
+    for (int l = 0; l < L; l++) {
+        const g3attn_layer_weights *lw = &w->layers[l];
+        if (!lw->input_layernorm || !lw->q_proj || !lw->k_proj || !lw->v_proj || !lw->o_proj ||
+            !lw->gate_proj || !lw->up_proj || !lw->down_proj) {
+            set_err("g3attn_prefill_forward_device: layer %d has a null projection or input norm", l);
+            return G3_ERR_INVALID_ARG;
+        }
+    }
+    if ((long long)start_pos + num_tokens > c->max_context) {
+        set_err("g3attn_prefill_forward_device: positions %d..%d exceed max_context %d", start_pos,
+                start_pos + num_tokens - 1, c->max_context);
+        return G3_ERR_CONTEXT_OVERFLOW;
+    }
+    for (int i = 0; i < num_tokens; i++)
+        if (tokens[i] < 0 || tokens[i] >= cfg->vocab_size) {
+            set_err("g3attn_prefill_forward_device: token %d at %d outside the vocabulary (%d)", tokens[i], i,
+                    cfg->vocab_size);
+            return G3_ERR_INVALID_ARG;
+        }
+    hipSetDevice(c->device);
+    const int chunk = num_tokens < PB_CHUNK ? num_tokens : PB_CHUNK;
+    pb_bufs b;
+    int rc = pb_layout(c, chunk, &b);
+    if (rc) return rc;
+    if ((size_t)chunk * sizeof(int) > c->d_tok_cap) {
+        HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_prefill_forward_device");
+        hipFree(c->d_tok);
+        c->d_tok = NULL;
+        c->d_tok_cap = 0;
+        if (!alloc_dev((void **)&c->d_tok, (size_t)chunk * sizeof(int), "prefill tokens")) return G3_ERR_OUT_OF_MEMORY;
+        c->d_tok_cap = (size_t)chunk * sizeof(int);
+    }
+    int last_n = 0;
+    for (int p = 0; p < num_tokens; p += chunk) {
+        const int n = num_tokens - p < chunk ? num_tokens - p : chunk;
+        /* the previous chunk's kernels may still read the token ids */
+        HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_prefill_forward_device");
+        HIP_TRY(hipMemcpy(c->d_tok, tokens + p, (size_t)n * sizeof(int), hipMemcpyHostToDevice),
+                "g3attn_prefill_forward_device tokens");
+        if ((rc = prefill_chunk(c, w, n, start_pos + p, &b))) return rc;
+        last_n = n;
+    }
+    if (logits) {
+        /* the last token's final norm and tied logits (:769-773) */
+        float *xl = b.x + (size_t)(last_n - 1) * hid;
+        if ((rc = layer_step(c, G3K_OP_NORM, xl, NULL, b.xn, NULL, w->norm, NULL, 0))) return rc;
+        if ((rc = gemv(c, logits, w->embed_tokens, b.xn, cfg->vocab_size, hid))) return rc;
+    }
+    return G3_OK;
+}
+
 /* ---------------------------------------------------------- uploaded model */
 
 /* Element counts of the 13 per-layer tensors in the g3attn_layer_weights
@@ -1181,6 +1474,20 @@ int g3attn_upload_weights(g3attn_ctx *c, const void *weights) {
 
 const g3attn_weights *g3attn_device_weights(g3attn_ctx *c) { return c && c->have_wt ? &c->wt : NULL; }
 
+/* The device logits of the host-output calls and their pinned staging. */
+static int forward_uploaded_logits(g3attn_ctx *c, const char *who) {
+    const size_t vb = (size_t)c->cfg.vocab_size * sizeof(float);
+    if (!alloc_dev((void **)&c->d_logits, vb, "logits")) return G3_ERR_OUT_OF_MEMORY;
+    if (hipHostMalloc((void **)&c->h_logits, vb, 0) != hipSuccess) {
+        c->h_logits = NULL;
+        hipFree(c->d_logits);
+        c->d_logits = NULL;
+        set_err("%s: pinned logits allocation failed", who);
+        return G3_ERR_OUT_OF_MEMORY;
+    }
+    return G3_OK;
+}
+
 /* Enqueue one token on the uploaded model; when want_logits, its logits land
  * in c->d_logits. */
 static int forward_uploaded(g3attn_ctx *c, int token_id, int pos, int want_logits, const char *who) {
@@ -1189,13 +1496,8 @@ static int forward_uploaded(g3attn_ctx *c, int token_id, int pos, int want_logit
         return G3_ERR_INVALID_ARG;
     }
     if (want_logits && !c->d_logits) {
-        const size_t vb = (size_t)c->cfg.vocab_size * sizeof(float);
-        if (!alloc_dev((void **)&c->d_logits, vb, "logits")) return G3_ERR_OUT_OF_MEMORY;
-        if (hipHostMalloc((void **)&c->h_logits, vb, 0) != hipSuccess) {
-            c->h_logits = NULL;
-            set_err("%s: pinned logits allocation failed", who);
-            return G3_ERR_OUT_OF_MEMORY;
-        }
+        const int rc = forward_uploaded_logits(c, who);
+        if (rc) return rc;
     }
     return g3attn_forward_device(c, &c->wt, token_id, pos, want_logits ? c->d_logits : NULL, want_logits, NULL);
 }
@@ -1239,8 +1541,23 @@ int g3attn_prefill_tokens(g3attn_ctx *c, const int *tokens, int num_tokens, int 
             return G3_ERR_INVALID_ARG;
         }
     hipSetDevice(c->device);
-    /* every token is enqueued without a host round trip; only the last one
-     * computes logits (gemma3_metal.m:977-987) */
+    if (num_tokens >= G3ATTN_PREFILL_BATCH_MIN) {
+        /* the batched prefill (gemma3_transformer.c:526-787): projections as
+         * MFMA GEMMs, attention on the prefill kernel */
+        if (!c->have_wt) {
+            set_err("g3attn_prefill_tokens: no weights uploaded (g3attn_upload_weights)");
+            return G3_ERR_INVALID_ARG;
+        }
+        int rc = G3_OK;
+        if (logits && !c->d_logits) rc = forward_uploaded_logits(c, "g3attn_prefill_tokens");
+        if (!rc) rc = g3attn_prefill_forward_device(c, &c->wt, tokens, num_tokens, start_pos, logits ? c->d_logits : NULL);
+        if (rc) return rc;
+        if (logits) return logits_to_host(c, logits, "g3attn_prefill_tokens");
+        HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_prefill_tokens");
+        return G3_OK;
+    }
+    /* a short batch: every token is enqueued without a host round trip; only
+     * the last one computes logits (gemma3_metal.m:977-987) */
     for (int i = 0; i < num_tokens; i++) {
         const int last = i == num_tokens - 1;
         const int rc = forward_uploaded(c, tokens[i], start_pos + i, last && logits, "g3attn_prefill_tokens");

@@ -244,10 +244,36 @@ int g3attn_forward_token(g3attn_ctx *ctx, int token_id, int pos, float *logits, 
 
 /* gemma3_metal_prefill (gemma3_metal.m:977-987), gemma3_transformer_
  * prefill_tokens' backend branch (:953-958): tokens[0..n-1] at positions
- * start_pos.. through the uploaded model, enqueued back to back; logits (host,
- * may be NULL) receives the last token's logits.  Tokens and positions are
- * checked before anything is enqueued.  Blocking. */
+ * start_pos.. through the uploaded model; logits (host, may be NULL) receives
+ * the last token's logits.  Tokens and positions are checked before anything
+ * is enqueued.  Batches of G3ATTN_PREFILL_BATCH_MIN tokens or more take the
+ * batched path (g3attn_prefill_forward_device, the USE_BLAS build's
+ * gemma3_transformer_prefill_batched); shorter ones run the token forward
+ * back to back.  Blocking. */
+#define G3ATTN_PREFILL_BATCH_MIN 16
 int g3attn_prefill_tokens(g3attn_ctx *ctx, const int *tokens, int num_tokens, int start_pos, float *logits);
+
+/* The batched prefill's projection, C = X . W^T: the reference's
+ * bf16_matrix_to_f32 + cblas_sgemm(RowMajor, NoTrans, Trans, N, M, K, 1, X, K,
+ * W_f32, K, 0, C, M) pairs (gemma3_transformer.c:614-639, 694-699, 726-751).
+ * X [N][K] fp32, W [M][K] bf16, C [N][M] fp32, device pointers; M a multiple
+ * of 4, K of 32.  On MFMA: X is split into bf16 hi + lo planes (relative error
+ * <= 2^-17) and both are multiplied by W with fp32 accumulation.  Enqueued on
+ * the context stream. */
+int g3attn_matmul_bf16_device(g3attn_ctx *ctx, float *C, const uint16_t *W, const float *X, int N, int M, int K);
+
+/* gemma3_transformer_prefill_batched (gemma3_transformer.c:526-787) on the
+ * GPU: all num_tokens tokens (host array) through each layer at once, in
+ * chunks of up to 8192.  The reference's bf16 -> fp32 conversions and
+ * cblas_sgemm calls (:614-639, 694-699, 726-751) become MFMA GEMMs (bf16
+ * weights times the fp32 activations as bf16 hi + lo planes, fp32
+ * accumulation); the per-token attention loop (:641-692) is g3attn_prefill's
+ * kernel; the norms and residuals run per token row.  weights holds device
+ * pointers; logits (device, [vocab_size], may be NULL) receives the last
+ * token's logits.  Hidden and intermediate sizes must be multiples of 32.
+ * Enqueued on the context stream. */
+int g3attn_prefill_forward_device(g3attn_ctx *ctx, const g3attn_weights *weights, const int *tokens,
+                                  int num_tokens, int start_pos, float *logits);
 
 /* The context's HIP stream (hipStream_t), for callers that interleave their
  * own work; and a wait for everything queued on it. */

@@ -186,12 +186,13 @@ def test_upload_from_a_file_mapping(tmp_path):
 
 
 def test_prefill_tokens_equals_the_token_loop():
-    """prefill_tokens enqueues the tokens back to back and returns the last
-    token's logits: bit-identical to forward_token one by one, and decoding
-    continues from it identically."""
+    """A batch shorter than G3ATTN_PREFILL_BATCH_MIN: prefill_tokens enqueues
+    the tokens back to back and returns the last token's logits, bit-identical
+    to forward_token one by one, and decoding continues from it identically.
+    (Longer batches take the batched path: tests/test_gpu_gemm.py.)"""
     cfg, f, embed, layers, norm, tokens = MG.forward_case()
     HW, keep = G.host_weights(embed, layers, norm)
-    n = 25
+    n = 12
     with G.Context(_gpu_config(f), f["max_context"]) as a, G.Context(_gpu_config(f), f["max_context"]) as b:
         a.upload_weights(HW)
         b.upload_weights(HW)

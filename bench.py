@@ -570,6 +570,33 @@ def main():
         t_host = (time.perf_counter() - t0) / 20
         assert np.all(np.isfinite(lh))
         extra["forward_token_pos8191"]["host_logits_ms_per_token"] = round(t_host * 1e3, 3)
+
+        # the batched prefill (MFMA projections + the prefill attention kernel)
+        # of configs[2]'s length through the whole model
+        for ntok in (2048, 8192):
+            toks = (np.arange(ntok, dtype=np.int32) * 7919 % (vocab - 2) + 2).astype(np.int32)
+
+            def pf(toks=toks):
+                ctx.prefill_forward_device(W, toks, 0, logits.data_ptr())
+            steps = 4 if ntok == 2048 else 2
+            region, _, _ = B.time_calls(ctx, [pf], steps, 1)
+            assert bool(torch.isfinite(logits).all())
+            t = region / steps
+            gemm_flops = 2.0 * ntok * nl * (layer_w // 2)
+            attn_flops = sum(prefill_flops(ntok, 1 << 30 if G.is_global_layer(l) else cfg.sliding_window)
+                             for l in range(nl))
+            extra[f"prefill_model_N{ntok}"] = {
+                "config": f"g3attn_prefill_forward_device: {ntok} tokens from position 0 through all 34 "
+                          "layers + the last token's logits, Gemma3-4B shapes, random bf16 weights; "
+                          "projections as MFMA GEMMs (x as bf16 hi + lo: 2x the algorithmic MFMA work)",
+                "ms": round(t * 1e3, 2),
+                "tokens_per_s": round(ntok / t, 1),
+                "projection_TFLOP": round(gemm_flops / 1e12, 2),
+                "attention_TFLOP": round(attn_flops / 1e12, 3),
+                "TFLOP/s": round((gemm_flops + attn_flops) / t / 1e12, 1),
+                "frac_of_bf16_peak": round((gemm_flops + attn_flops) / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            }
+            log(f"[bench] prefill model: {extra[f'prefill_model_N{ntok}']}")
         ctx.close()
 
     # ---------------- prefill.  The configs' inputs are

@@ -99,6 +99,12 @@ __device__ __forceinline__ void store16(float *dst, const float (&x)[4][4], int 
 }
 
 
+// One cache row's 16 dims of this lane.  Plain loads: non-temporal ones were
+// measured faster (6.75 vs 6.0 TB/s at 128K) but returned stale values for
+// rows that a host -> device copy rewrote after a kernel had read them
+// (tests/test_gpu_decode.py::test_cache_rewritten_by_copy).
+__device__ __forceinline__ void load16_stream(float (&x)[4][4], const float *src, int c) { load16(x, src, c); }
+
 template <int R>
 __device__ __forceinline__ void load_step(float (&kk)[R][4][4], float (&vv)[R][4][4],
                                           const float *kbase, const float *vbase, long long rs,
@@ -108,13 +114,13 @@ __device__ __forceinline__ void load_step(float (&kk)[R][4][4], float (&vv)[R][4
     for (int r = 0; r < R; r++) {
         const int idx = base + grp * R + r;
         const int row = idx < c1 ? idx + (idx >= skip) : base_row;
-        load16(kk[r], kbase + (size_t)row * rs, c);
+        load16_stream(kk[r], kbase + (size_t)row * rs, c);
     }
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const int idx = base + grp * R + r;
         const int row = idx < c1 ? idx + (idx >= skip) : base_row;
-        load16(vv[r], vbase + (size_t)row * rs, c);
+        load16_stream(vv[r], vbase + (size_t)row * rs, c);
     }
 }
 

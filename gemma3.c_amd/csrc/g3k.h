@@ -186,7 +186,8 @@ int g3k_layer_step(const g3k_layer_args *a, void *stream);
  *                      x[r] += t'; then, if y_hi: y[r] = rmsnorm(x[r], w_next),
  *                      or x[r] itself if w_next is NULL
  *   G3K_ROWS_SPLIT:    y[r] = t[r] (any n; the other ops take n <= G3K_LAYER_MAX_HIDDEN)
- * x is [rows][n] fp32, t [rows][ldt] fp32, y_hi / y_lo [rows][ldy] bf16;
+ * x is [rows][n] fp32, t [rows][ldt] fp32 (RESIDUAL: the sum of nsplit >= 1
+ * partial products at t + s * split_stride), y_hi / y_lo [rows][ldy] bf16;
  * tokens is a device array. */
 enum { G3K_ROWS_EMBED = 0, G3K_ROWS_RESIDUAL = 1, G3K_ROWS_SPLIT = 2 };
 typedef struct {
@@ -196,7 +197,8 @@ typedef struct {
     const uint16_t *embed, *w_post, *w_next;
     float *x;
     const float *t;
-    int ldt;
+    int ldt, nsplit;
+    long long split_stride;
     uint16_t *y_hi, *y_lo;
     int ldy;
 } g3k_rows_args;
@@ -204,13 +206,17 @@ typedef struct {
 int g3k_rows(const g3k_rows_args *a, void *stream);
 
 /* Batched projection on MFMA: C[n][m] = sum_k X[n][k] W[m][k] for N tokens,
- * X given as bf16 planes x_hi + x_lo [N][ldx], W bf16 [M][K] (K % 32 == 0,
- * M % 4 == 0).  mode 0: n_mat (1..3) matrices sharing X, each written to
- * C[j] [N][ldc[j]] fp32.  mode G3K_MV_GEGLU: W[0] = gate, W[1] = up (same M);
- * gelu_tanh(gate) * up is written as bf16 planes h_hi + h_lo [N][ldh]. */
+ * X given as bf16 planes x_hi + x_lo [N][ldx], W bf16 [M][K] (K % (32 ksplit)
+ * == 0, M % 4 == 0).  mode 0: n_mat (1..3) matrices sharing X, each written
+ * to C[j] [N][ldc[j]] fp32; with ksplit S > 1, split s covers k in
+ * [s K / S, (s + 1) K / S) and writes its partial product to C[j] +
+ * s * split_stride (floats), for the consumer to add.  mode G3K_MV_GEGLU
+ * (ksplit 1): W[0] = gate, W[1] = up (same M); gelu_tanh(gate) * up is
+ * written as bf16 planes h_hi + h_lo [N][ldh]. */
 typedef struct {
     const uint16_t *x_hi, *x_lo;
-    int N, K, ldx, n_mat, mode;
+    int N, K, ldx, n_mat, mode, ksplit;
+    long long split_stride;
     const uint16_t *W[G3K_MATVEC_MAX];
     int M[G3K_MATVEC_MAX];
     float *C[G3K_MATVEC_MAX];

@@ -225,6 +225,14 @@ __global__ __launch_bounds__(RNT) void rows_kernel(g3k_rows_args a) {
             tv[u] = i < n ? t[i] : 0.f;
             v[u] = i < n ? x[i] : 0.f;
         }
+        for (int s = 1; s < a.nsplit; s++) {   // the k splits of the producing GEMM, in order
+            const float *ts = t + (size_t)s * a.split_stride;
+#pragma unroll
+            for (int u = 0; u < RPER; u++) {
+                const int i = threadIdx.x + RNT * u;
+                if (i < n) tv[u] += ts[i];
+            }
+        }
         if (a.w_post) {
             float ss = 0.f;
 #pragma unroll
@@ -265,7 +273,8 @@ extern "C" int g3k_rows(const g3k_rows_args *a, void *stream) {
             if (!a->tokens || !a->embed || !a->x || !split_out) return (int)hipErrorInvalidValue;
             break;
         case G3K_ROWS_RESIDUAL:
-            if (!a->x || !a->t || a->ldt < a->n || ((a->y_hi || a->y_lo) && !split_out))
+            if (!a->x || !a->t || a->ldt < a->n || ((a->y_hi || a->y_lo) && !split_out) || a->nsplit < 1 ||
+                (a->nsplit > 1 && a->split_stride < (long long)a->rows * a->ldt))
                 return (int)hipErrorInvalidValue;
             break;
         case G3K_ROWS_SPLIT:

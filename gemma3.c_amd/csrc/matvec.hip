@@ -12,9 +12,8 @@
 // Workgroup = 4 waves; each wave owns RPW consecutive rows.  Lane l reads the
 // 16-byte chunks l + 64 j of each row (8 elements each), so one wave load
 // covers 1 KiB of a row, contiguous; CH chunks per lane (a round) are issued,
-// with the x chunks they meet, before the FMAs that use them.  A is streamed
-// with non-temporal loads: every byte is read once, and keeping it out of the
-// caches leaves them to x.  Row sums reduce over the wave with DPP and
+// with the x chunks they meet, before the FMAs that use them.  Row sums
+// reduce over the wave with DPP and
 // permlane swaps.  Rows whose length is not a multiple of 8 (or unaligned
 // buffers) take a lane-strided scalar path.
 //
@@ -75,13 +74,11 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// 16 bytes of A, non-temporal (read once).
-__device__ __forceinline__ uint4 load_a(const uint16_t *p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
+// 16 bytes of A.  Plain loads: non-temporal ones stream faster, but the
+// decode kernel's measurements showed them returning stale values for memory
+// that a host -> device copy rewrote after kernels had touched it, and A may
+// be re-uploaded in place (g3attn_upload_weights, a caller's own buffers).
+__device__ __forceinline__ uint4 load_a(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
 // NA dot products per wave: RPW consecutive rows of one matrix, or (GEGLU)
 // the same row of the gate and up matrices.  XLDS: x is copied to LDS by the

@@ -1099,6 +1099,7 @@ int g3attn_matmul_bf16_device(g3attn_ctx *c, float *C, const uint16_t *W, const 
     g.K = K;
     g.ldx = K;
     g.n_mat = 1;
+    g.ksplit = 1;
     g.W[0] = W;
     g.M[0] = M;
     g.C[0] = C;
@@ -1113,6 +1114,17 @@ int g3attn_matmul_bf16_device(g3attn_ctx *c, float *C, const uint16_t *W, const 
 /* Tokens per pass through the stack: the activations below take about 100 KiB
  * per token at Gemma3-4B shapes (0.8 GiB at 8192). */
 #define PB_CHUNK 8192
+#define PB_SPLIT_MAX 4
+
+/* k splits for a GEMM with M output rows over n tokens: the smallest power of
+ * two (<= PB_SPLIT_MAX) that gives 512 workgroups of 128 x 128 (two per CU),
+ * with K / S a multiple of 32. */
+static int pick_ksplit(int n, int M, int K) {
+    const long long wgs = (long long)((M + 127) / 128) * ((n + 127) / 128);
+    int S = 1;
+    while (S < PB_SPLIT_MAX && wgs * S < 512 && K % (32 * 2 * S) == 0) S *= 2;
+    return S;
+}
 
 typedef struct {
     float *x, *q, *k, *v, *attn, *t, *xn;
@@ -1123,7 +1135,7 @@ static int pb_layout(g3attn_ctx *c, int n, pb_bufs *b) {
     const g3attn_config *cfg = &c->cfg;
     const size_t hid = cfg->hidden_size, inter = cfg->intermediate_size;
     const size_t qs = (size_t)cfg->num_heads * D, ks = (size_t)cfg->num_kv_heads * D, N = n;
-    const size_t sz[13] = {N * hid * 4, N * qs * 4, N * ks * 4, N * ks * 4, N * qs * 4, N * hid * 4, hid * 4,
+    const size_t sz[13] = {N * hid * 4, N * qs * 4, N * ks * 4, N * ks * 4, N * qs * 4, PB_SPLIT_MAX * N * hid * 4, hid * 4,
                            N * hid * 2, N * hid * 2, N * qs * 2, N * qs * 2, N * inter * 2, N * inter * 2};
     size_t total = 0;
     for (int i = 0; i < 13; i++) total += align256(sz[i]);
@@ -1184,6 +1196,7 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         g.K = hid;
         g.ldx = hid;
         g.n_mat = 3;
+        g.ksplit = 1;
         g.W[0] = lw->q_proj;
         g.W[1] = lw->k_proj;
         g.W[2] = lw->v_proj;
@@ -1216,11 +1229,14 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         g.K = qs;
         g.ldx = qs;
         g.n_mat = 1;
+        g.ksplit = pick_ksplit(n, hid, qs);
+        g.split_stride = (long long)n * hid;
         g.W[0] = lw->o_proj;
         g.M[0] = hid;
         g.C[0] = b->t;
         g.ldc[0] = hid;
         if ((rc = gemm_step(c, &g))) return rc;
+        const int o_split = g.ksplit;
         /* post-attention norm + residual, pre-feedforward norm (:701-724) */
         memset(&r, 0, sizeof r);
         r.op = G3K_ROWS_RESIDUAL;
@@ -1232,6 +1248,8 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         r.x = b->x;
         r.t = b->t;
         r.ldt = hid;
+        r.nsplit = o_split;
+        r.split_stride = (long long)n * hid;
         r.y_hi = b->xh;
         r.y_lo = b->xl;
         r.ldy = hid;
@@ -1244,6 +1262,7 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         g.K = hid;
         g.ldx = hid;
         g.n_mat = 2;
+        g.ksplit = 1;
         g.mode = G3K_MV_GEGLU;
         g.W[0] = lw->gate_proj;
         g.W[1] = lw->up_proj;
@@ -1260,11 +1279,14 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         g.K = inter;
         g.ldx = inter;
         g.n_mat = 1;
+        g.ksplit = pick_ksplit(n, hid, inter);
+        g.split_stride = (long long)n * hid;
         g.W[0] = lw->down_proj;
         g.M[0] = hid;
         g.C[0] = b->t;
         g.ldc[0] = hid;
         if ((rc = gemm_step(c, &g))) return rc;
+        const int d_split = g.ksplit;
         /* post-feedforward norm + residual (:753-765), then the next layer's input norm */
         const int last = l + 1 == L;
         memset(&r, 0, sizeof r);
@@ -1277,6 +1299,8 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         r.x = b->x;
         r.t = b->t;
         r.ldt = hid;
+        r.nsplit = d_split;
+        r.split_stride = (long long)n * hid;
         r.y_hi = last ? NULL : b->xh;
         r.y_lo = last ? NULL : b->xl;
         r.ldy = hid;

@@ -51,6 +51,15 @@ def test_config1_local_decode(ctx8k):
     _check(DecodeCase(1, layer=0, pos=511, max_context=8192), ctx8k, "config1")
 
 
+def test_cache_rewritten_by_copy(ctx8k):
+    """Cache rows that a decode has read, then rewritten by a host -> device
+    copy (g3attn_kv_write), are read back fresh by the next decode: two
+    different histories in the same slots, each against its own oracle."""
+    for layer_seed in (0, 7, 0):
+        _check(DecodeCase(1, layer=11, pos=700, max_context=8192, layer_seed=layer_seed), ctx8k,
+               f"rewrite-{layer_seed}")
+
+
 def test_config2_global_decode(ctx8k):
     """global layer, pos 8191, L = 8192."""
     _check(DecodeCase(2, layer=5, pos=8191, max_context=8192), ctx8k, "config2")

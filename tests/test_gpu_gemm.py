@@ -49,10 +49,12 @@ def _check_gemm(C, W, X, label):
 
 @pytest.mark.parametrize("N,M,K", [(1, 4, 32), (5, 12, 64), (130, 260, 96), (16, 128, 32),
                                    (257, 2048, 2560), (64, 1028, 10240), (300, 4, 32),
-                                   (129, 132, 2048)])
+                                   (129, 132, 2048), (4096, 4096, 512)])
 def test_matmul_matches_fp64(N, M, K):
     """Full and ragged tiles in both dimensions (rows past M or N read zero),
-    one K step, the projections' K (hidden 2560, q 2048, intermediate 10240)."""
+    one K step, the projections' K (hidden 2560, q 2048, intermediate 10240),
+    and a launch large enough for the 256-row tiles (>= 512 workgroups).
+    Split-K (o_proj, down_proj) runs in the batched-prefill tests below."""
     rng = np.random.default_rng(N * 7 + M * 13 + K)
     W = MG.weights_bf16(M, K, 0xE000 + M + K)
     X = rng.standard_normal((N, K)).astype(np.float32)

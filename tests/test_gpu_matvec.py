@@ -139,6 +139,24 @@ def test_layer_attention_single_entry_point():
     assert err < 1e-4
 
 
+def test_weights_rewritten_by_copy():
+    """The GEMV streams A with non-temporal loads.  A matrix read by a GEMV,
+    then overwritten in place by a host -> device copy, must be read fresh
+    by the next GEMV (several rounds, each against its own reference)."""
+    with G.Context(G.default_config(max_context=1024, num_layers=6), 1024) as ctx:
+        M, K = 2560, 2560
+        dA, dx, dy = DeviceBuffer(M * K * 2), DeviceBuffer(K * 4), DeviceBuffer(M * 4)
+        x = O.gen_normal_bf16(K, 0xB400)
+        dx.upload(x)
+        for rnd in range(4):
+            A = MG.weights_bf16(M, K, 0xB500 + rnd)
+            dA.upload(A)
+            ctx.matvec_bf16_device(dy.ptr, dA.ptr, dx.ptr, M, K)
+            ctx.synchronize()
+            _check(dy.download(np.float32, M), O.matvec_bf16(A, x).astype(np.float64), A, x,
+                   f"rewrite-{rnd}")
+
+
 def test_matvec_errors():
     A = np.zeros((2, 8), np.uint16)
     with pytest.raises(G.G3AttnError):

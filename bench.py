@@ -27,6 +27,14 @@ global prefill (N=8192).  Prefill FLOPs are algorithmic: 4 * H_q * d * P for
 P attended (query, key) pairs; the MFMA kernel issues 2.5x that (three fp16
 passes for QK^T, two bf16 passes for PV), reported as "issued".
 
+The rows beyond the attention block, at Gemma3-4B shapes with random bf16
+weights (sections `gemv` and `forward`): one layer's Q/K/V + O projection
+GEMVs, the whole layer_attention at pos 8191, the model's upload from host
+memory, one token through all 34 layers with the tied logits (HBM GB/s over
+every weight byte plus the cache rows read), and the batched prefill of 2048
+and 8192 tokens through the model (algorithmic TFLOP/s; its projections issue
+2x their FLOPs on MFMA, x being carried as bf16 hi + lo).
+
 `cpu_baseline`: the reference's own attention code (oracle/_ref, compiled
 from the reference sources with its fast-mode flags, no BLAS) timed on one
 host core for the headline workload: median of 20 decode steps.
@@ -129,14 +137,21 @@ class Bench:
         self.torch.cuda.synchronize()
         return qkv, zn
 
-    def time_calls(self, stream_ctx, calls, steps, warmup):
+    def time_calls(self, stream_ctx, calls, steps, warmup, prewarm_s=0.0):
         """Run `calls[i % len]` for warmup + steps on the library stream.
         Returns (region seconds, mean per-call seconds, host wall seconds): the
         region is bracketed by two events only, so back-to-back calls run as an
         engine would issue them; per-call times come from a second pass with an
-        event pair around every call."""
+        event pair around every call.  prewarm_s: first run the calls for that
+        long (the part's clocks take tens of ms of MFMA load to settle: the
+        first prefill calls run 15-25% slower than the settled ones)."""
         torch = self.torch
         s = torch.cuda.ExternalStream(stream_ctx.stream())
+        t_end = time.perf_counter() + prewarm_s
+        while time.perf_counter() < t_end:
+            for f in calls:
+                f()
+            stream_ctx.synchronize()
         for i in range(warmup):
             calls[i % len(calls)]()
         stream_ctx.synchronize()
@@ -579,7 +594,7 @@ def main():
             def pf(toks=toks):
                 ctx.prefill_forward_device(W, toks, 0, logits.data_ptr())
             steps = 4 if ntok == 2048 else 2
-            region, _, _ = B.time_calls(ctx, [pf], steps, 1)
+            region, _, _ = B.time_calls(ctx, [pf], steps, 1, prewarm_s=0.2)
             assert bool(torch.isfinite(logits).all())
             t = region / steps
             gemm_flops = 2.0 * ntok * nl * (layer_w // 2)
@@ -619,7 +634,7 @@ def main():
         def pf(ctx=ctx, layer=layer, n=n, Q=Q, K=K, V=V, zn16=zn16, pout=pout):
             ctx.prefill_device(layer, 0, n, Q.data_ptr(), K.data_ptr(), V.data_ptr(),
                                zn16.data_ptr(), zn16.data_ptr(), pout.data_ptr())
-        region, per_call, _ = B.time_calls(ctx, [pf], steps, 3)
+        region, per_call, _ = B.time_calls(ctx, [pf], steps, 3, prewarm_s=0.2)
         k_s = B.kernel_time(ctx, [pf], steps, 1)
         flops = prefill_flops(n, window)
         extra[name] = {

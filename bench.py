@@ -243,6 +243,58 @@ def cpu_baseline(L=8192, reps=20):
     }
 
 
+def _oracle():
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import g3_oracle as O
+    return O
+
+
+def cpu_gemv_baseline(hid=2560, layers=8, reps=3):
+    """The reference's gemma3_matvec_bf16 (oracle/_ref) on one host core for
+    one layer's Q, K, V and O projections (the GEMV row's workload), rotating
+    over `layers` distinct layers' matrices so that they stream from DRAM."""
+    O = _oracle()
+    if not O.have_ref():
+        return None
+    pool = (np.random.default_rng(7).standard_normal(1 << 22) * 2.0 ** -6).astype(np.float32)
+    pool = (pool.view(np.uint32) >> 16).astype(np.uint16)
+    shapes = ((QS, hid), (KS, hid), (KS, hid), (hid, QS))
+    mats = [[np.resize(np.roll(pool, 997 * (4 * l + j)), sh) for j, sh in enumerate(shapes)] for l in range(layers)]
+    xs = [np.random.default_rng(8).standard_normal(sh[1]).astype(np.float32) for sh in shapes]
+    ts = []
+    for r in range(reps + 1):
+        a = time.perf_counter()
+        for lm in mats:
+            for m, x in zip(lm, xs):
+                O.matvec_bf16(m, x, use_ref=True)
+        if r:
+            ts.append((time.perf_counter() - a) / layers)
+    sec = float(np.median(ts))
+    byts = sum(m.nbytes for m in mats[0])
+    return {"value": round(byts / sec / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"median of {reps} passes over {layers} distinct layers' four projection matrices "
+                      f"({layers * byts / 1e6:.0f} MB): {sec * 1e3:.2f} ms per layer, gemma3_matvec_bf16, "
+                      "1 thread"}
+
+
+def cpu_forward_baseline(HW, cfg, pos, n_tokens=2):
+    """The reference's gemma3_transformer_forward (oracle/_ref, one thread, no
+    BLAS) on the same host weights: seconds per token at positions pos.."""
+    O = _oracle()
+    if not O.have_ref():
+        return None
+    L = cfg.num_layers
+    ptrs = (C.c_void_p * (13 * L))()
+    names = [n for n, _ in type(HW.layers[0])._fields_]
+    for l in range(L):
+        for j, n in enumerate(names):
+            ptrs[13 * l + j] = getattr(HW.layers[l], n)
+    sec = O.ref().ref_time_forward(HW.embed_tokens, ptrs, HW.norm, cfg.vocab_size, cfg.hidden_size,
+                                   cfg.intermediate_size, L, cfg.num_heads, cfg.num_kv_heads,
+                                   cfg.max_context, cfg.sliding_window, pos, n_tokens)
+    return None if sec <= 0 else sec
+
+
 def cpu_prefill_baseline():
     """The reference's prefill attention loop (gemma3_transformer.c:641-692 order,
     gemma3_gqa per token) on one host core, configs[2] in full (about 2 s)."""
@@ -470,6 +522,8 @@ def main():
             "GB/s": round(gemv_bytes / (region / 340) / 1e9, 1),
             "frac_of_hbm_peak": round(gemv_bytes / (region / 340) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        if not args.no_cpu:
+            extra["gemv_qkv_o_projections"]["cpu_baseline"] = cpu_gemv_baseline(hid)
         log(f"[bench] gemv: {extra['gemv_qkv_o_projections']}")
         # the whole of layer_attention at configs[1]'s position: projections +
         # attention over 8192 cached positions + o_proj, one entry point
@@ -540,7 +594,6 @@ def main():
         t0 = time.perf_counter()
         ctx.upload_weights(HW)
         up_s = time.perf_counter() - t0
-        del host
         extra["weight_upload"] = {
             "config": "g3attn_upload_weights of the whole Gemma3-4B-shaped model (every bf16 tensor, "
                       "%.2f GB) from pageable host memory through two pinned 32 MiB staging buffers"
@@ -585,6 +638,25 @@ def main():
         t_host = (time.perf_counter() - t0) / 20
         assert np.all(np.isfinite(lh))
         extra["forward_token_pos8191"]["host_logits_ms_per_token"] = round(t_host * 1e3, 3)
+        if not args.no_cpu:
+            # the reference's token forward on the same weights (host copy), one thread
+            log("[bench] cpu forward baseline (reference, 1 core, 2 tokens at pos 8190-8191 "
+                "and 2 at pos 1023-1024)")
+            s_hi = cpu_forward_baseline(HW, cfg, pos - 1)
+            s_lo = cpu_forward_baseline(HW, cfg, 1023)
+            if s_hi:
+                extra["forward_token_pos8191"]["cpu_baseline"] = {
+                    "value": round(1.0 / s_hi, 3), "unit": "tokens/s", "cores": 1, "kind": "reference",
+                    "sample": f"gemma3_transformer_forward, median of 2 tokens at pos 8190-8191 after one "
+                              f"warm-up token: {s_hi:.2f} s per token, 1 thread, no BLAS, same weights"}
+            if s_lo:
+                extra["cpu_prefill_model_token_loop"] = {
+                    "value": round(1.0 / s_lo, 3), "unit": "tokens/s", "cores": 1, "kind": "reference",
+                    "sample": f"the non-BLAS reference prefill is this token loop "
+                              f"(gemma3_transformer.c:814-821): gemma3_transformer_forward at pos "
+                              f"1023-1024, {s_lo:.2f} s per token, 1 thread (the BLAS build's batched "
+                              f"prefill needs cblas.h, absent)"}
+        del host
 
         # the batched prefill (MFMA projections + the prefill attention kernel)
         # of configs[2]'s length through the whole model

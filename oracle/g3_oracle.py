@@ -174,6 +174,9 @@ def ref():
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                       C.c_int, C.c_int]
         R.ref_forward_seq.restype = C.c_int
+        R.ref_time_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        R.ref_time_forward.restype = C.c_double
         _ref = R
     return _ref
 

@@ -152,36 +152,91 @@ done:
  * bf16 weights (layer_w: num_layers x 13 tensors in the gemma3_weights_t
  * field order) and model shape.  logits [n][vocab] holds every step's
  * logits; hidden_last [hidden] the hidden state after the last step. */
+static int cmp_double(const void *a, const void *b);
+
+/* The model config and gemma3_weights_t of caller-given tensors. */
+static void harness_model(gemma3_config *cfg, gemma3_weights_t *w, const uint16_t *embed,
+                          const uint16_t *const *layer_w, const uint16_t *norm, int vocab, int hidden,
+                          int inter, int num_layers, int hq, int hkv, int max_context, int window) {
+    *cfg = harness_cfg(hq, hkv, max_context, window);
+    cfg->vocab_size = vocab;
+    cfg->hidden_size = hidden;
+    cfg->intermediate_size = inter;
+    cfg->num_layers = num_layers;
+    memset(w, 0, sizeof *w);
+    w->embed_tokens = embed;
+    w->norm = norm;
+    for (int l = 0; l < num_layers; l++) {
+        const uint16_t *const *t = layer_w + (size_t)l * 13;
+        w->layers[l].input_layernorm = t[0];
+        w->layers[l].q_proj = t[1];
+        w->layers[l].k_proj = t[2];
+        w->layers[l].v_proj = t[3];
+        w->layers[l].o_proj = t[4];
+        w->layers[l].q_norm = t[5];
+        w->layers[l].k_norm = t[6];
+        w->layers[l].post_attention_layernorm = t[7];
+        w->layers[l].gate_proj = t[8];
+        w->layers[l].up_proj = t[9];
+        w->layers[l].down_proj = t[10];
+        w->layers[l].pre_feedforward_layernorm = t[11];
+        w->layers[l].post_feedforward_layernorm = t[12];
+    }
+}
+
+/* CPU baseline of the whole-token forward: seconds per token of
+ * gemma3_transformer_forward (one thread, no BLAS) at positions pos ..
+ * pos + n_tokens - 1 of a cache whose earlier rows are zero (the attention's
+ * cost does not depend on their values); the median after one warm-up token. */
+double ref_time_forward(const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                        int vocab, int hidden, int inter, int num_layers, int hq, int hkv,
+                        int max_context, int window, int pos, int n_tokens) {
+    if (num_layers < 1 || num_layers > GEMMA3_NUM_LAYERS || n_tokens < 1 || pos < 1 ||
+        pos + n_tokens > max_context)
+        return -1.0;
+    gemma3_config cfg;
+    gemma3_weights_t w;
+    harness_model(&cfg, &w, embed, layer_w, norm, vocab, hidden, inter, num_layers, hq, hkv, max_context,
+                  window);
+    gemma3_kv_cache *cache = gemma3_kv_cache_alloc(&cfg, max_context);
+    activation_buffers *buf = alloc_buffers(&cfg);
+    float *rl = (float *)malloc((size_t)max_context * RH_D * 4);
+    float *rg = (float *)malloc((size_t)max_context * RH_D * 4);
+    float *logits = (float *)malloc((size_t)vocab * 4);
+    double *t = (double *)malloc((size_t)n_tokens * sizeof(double));
+    double med = -4.0;
+    if (cache && buf && rl && rg && logits && t) {
+        gemma3_rope_precompute(rl, max_context, RH_D, cfg.rope_theta_local);
+        gemma3_rope_precompute(rg, max_context, RH_D, cfg.rope_theta_global);
+        int rc = 0;
+        for (int r = -1; r < n_tokens && !rc; r++) {
+            const int p = r < 0 ? pos - 1 : pos + r;
+            struct timespec a, b;
+            clock_gettime(CLOCK_MONOTONIC, &a);
+            rc = gemma3_transformer_forward(logits, (p * 7919) % vocab, p, &w, cache, buf, &cfg, 1, rl, rg, NULL);
+            clock_gettime(CLOCK_MONOTONIC, &b);
+            if (r >= 0) t[r] = (b.tv_sec - a.tv_sec) + 1e-9 * (b.tv_nsec - a.tv_nsec);
+        }
+        if (!rc) {
+            qsort(t, (size_t)n_tokens, sizeof(double), cmp_double);
+            med = t[n_tokens / 2];
+        }
+    }
+    if (cache) gemma3_kv_cache_free(cache);
+    if (buf) free_buffers(buf);
+    free(rl); free(rg); free(logits); free(t);
+    return med;
+}
+
 int ref_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
                     const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
                     int vocab, int hidden, int inter, int num_layers, int hq, int hkv,
                     int max_context, int window) {
     if (num_layers < 1 || num_layers > GEMMA3_NUM_LAYERS) return -1;
-    gemma3_config cfg = harness_cfg(hq, hkv, max_context, window);
-    cfg.vocab_size = vocab;
-    cfg.hidden_size = hidden;
-    cfg.intermediate_size = inter;
-    cfg.num_layers = num_layers;
+    gemma3_config cfg;
     gemma3_weights_t w;
-    memset(&w, 0, sizeof w);
-    w.embed_tokens = embed;
-    w.norm = norm;
-    for (int l = 0; l < num_layers; l++) {
-        const uint16_t *const *t = layer_w + (size_t)l * 13;
-        w.layers[l].input_layernorm = t[0];
-        w.layers[l].q_proj = t[1];
-        w.layers[l].k_proj = t[2];
-        w.layers[l].v_proj = t[3];
-        w.layers[l].o_proj = t[4];
-        w.layers[l].q_norm = t[5];
-        w.layers[l].k_norm = t[6];
-        w.layers[l].post_attention_layernorm = t[7];
-        w.layers[l].gate_proj = t[8];
-        w.layers[l].up_proj = t[9];
-        w.layers[l].down_proj = t[10];
-        w.layers[l].pre_feedforward_layernorm = t[11];
-        w.layers[l].post_feedforward_layernorm = t[12];
-    }
+    harness_model(&cfg, &w, embed, layer_w, norm, vocab, hidden, inter, num_layers, hq, hkv, max_context,
+                  window);
     gemma3_kv_cache *cache = gemma3_kv_cache_alloc(&cfg, max_context);
     activation_buffers *buf = alloc_buffers(&cfg);
     float *rl = (float *)malloc((size_t)max_context * RH_D * 4);

@@ -9,18 +9,19 @@
 // and its output projection (:355).
 //
 // At decode batch 1 the GEMV is HBM-bound: 2 bytes of A per multiply-add.
-// Workgroup = 4 waves; each wave owns RPW consecutive rows.  Lane l reads the
-// 16-byte chunks l + 64 j of each row (8 elements each), so one wave load
-// covers 1 KiB of a row, contiguous; CH chunks per lane (a round) are issued,
-// with the x chunks they meet, before the FMAs that use them.  Row sums
-// reduce over the wave with DPP and
+// Workgroup = 4 waves.  Lane l reads the 16-byte chunks l + 64 j of a row
+// (8 elements each), so one wave load covers 1 KiB of the row, contiguous;
+// CH chunks per lane (a round) are issued, with the x chunks they meet,
+// before the FMAs that use them.  Sums reduce over the wave with DPP and
 // permlane swaps.  Rows whose length is not a multiple of 8 (or unaligned
 // buffers) take a lane-strided scalar path.
 //
-// Shapes pick the variant (measured on the forward's shapes): long rows
-// (K >= 8192, the MLP's down projection) stage x in LDS once per workgroup
-// instead of once per wave; rows of at most 2048 elements take 4 chunks per
-// round (one round); very tall matrices (the tied logits) take 2 rows per wave.
+// Two layouts, picked per shape (measured on the forward's shapes):
+//   each wave owns RPW rows of its own (the Q/K/V projections: 1 row, one
+//   round of 8 chunks at K = 2560; the tied logits, 262208 rows: 2 rows);
+//   or the 4 waves share RPW rows and split each row's chunks in four (KS):
+//   the down projection (K = 10240: 5 chunks per lane, one memory round trip
+//   instead of five), o_proj (K = 2048) and the GEGLU gate / up pair.
 //
 // One launch can serve up to three matrices that share x (the Q, K and V
 // projections of one token): workgroups are dealt to the matrices in order of
@@ -37,7 +38,6 @@ using namespace g3k;
 
 constexpr int NT = 256;   // 4 waves
 constexpr int NW = NT / 64;
-constexpr int G3K_MATVEC_LDS_MAX_K = 16384;
 
 __device__ __forceinline__ float dot8(uint4 w, float4 xa, float4 xb) {
     float s = bf16f(w.x & 0xffff) * xa.x;
@@ -80,27 +80,29 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // be re-uploaded in place (g3attn_upload_weights, a caller's own buffers).
 __device__ __forceinline__ uint4 load_a(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// NA dot products per wave: RPW consecutive rows of one matrix, or (GEGLU)
-// the same row of the gate and up matrices.  XLDS: x is copied to LDS by the
-// workgroup (dynamic shared memory of K floats) after the first round's A
-// loads are issued.
-template <int RPW, int CH, bool VEC, bool XLDS, bool GEGLU>
+// NA dot products: RPW consecutive rows of one matrix, or (GEGLU) the same
+// rows of the gate and up matrices.  Without KS each wave owns its own RPW
+// rows (a workgroup covers 4 RPW rows); with KS the workgroup's 4 waves share
+// RPW rows and wave w takes the w-th quarter of every row's chunks (one
+// memory round trip for long rows), the four partial sums meeting in LDS.
+template <int RPW, int CH, bool VEC, bool KS, bool GEGLU>
 __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
-    extern __shared__ float4 xs4[];
-    constexpr int NA = GEGLU ? 2 : RPW;
+    constexpr int NA = GEGLU ? 2 * RPW : RPW;
+    __shared__ float red[KS ? NW : 1][NA];
     const int K = a.K;
     int row0;
-    const int m = pick(a, NW * RPW, row0);
+    const int m = pick(a, KS ? RPW : NW * RPW, row0);
     if (m < 0) return;   // uniform over the workgroup
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int M = a.M[m];
     const float *x = a.x;
-    const int r0 = row0 + wave * RPW;
+    const int r0 = KS ? row0 : row0 + wave * RPW;
     const uint16_t *rows[NA];
 #pragma unroll
     for (int j = 0; j < NA; j++) {
-        const int row = GEGLU ? (r0 < M ? r0 : M - 1) : (r0 + j < M ? r0 + j : M - 1);
-        rows[j] = a.A[GEGLU ? j : m] + (size_t)row * K;
+        const int jr = GEGLU ? j % RPW : j;
+        const int row = r0 + jr < M ? r0 + jr : M - 1;
+        rows[j] = a.A[GEGLU ? j / RPW : m] + (size_t)row * K;
     }
     float acc[NA];
 #pragma unroll
@@ -108,64 +110,68 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
 
     if (VEC) {
         const int nch = K >> 3;
+        const int q = KS ? (nch + NW - 1) / NW : nch;
+        const int cbeg = KS ? wave * q : 0, cend = KS ? min(cbeg + q, nch) : nch;
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
-        // rounds are uniform over the workgroup (the LDS copy has a barrier)
-        for (int base = 0; base < nch; base += 64 * CH) {
+        for (int base = cbeg; base < cend; base += 64 * CH) {
             uint4 w[NA][CH];
             float4 xa[CH], xb[CH];
 #pragma unroll
             for (int u = 0; u < CH; u++) {
                 const int c = base + lane + 64 * u;
-                const bool ok = c < nch;
+                const bool ok = c < cend;
 #pragma unroll
-                for (int j = 0; j < NA; j++) w[j][u] = ok ? load_a(rows[j] + 8 * c) : make_uint4(0, 0, 0, 0);
-                if (!XLDS) {
-                    xa[u] = ok ? x4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    xb[u] = ok ? x4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-            }
-            if (XLDS && base == 0) {
-                for (int i = threadIdx.x; i < 2 * nch; i += NT) xs4[i] = x4[i];
-                __syncthreads();
+                for (int j = 0; j < NA; j++)
+                    w[j][u] = ok ? *reinterpret_cast<const uint4 *>(rows[j] + 8 * c) : make_uint4(0, 0, 0, 0);
+                xa[u] = ok ? x4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
+                xb[u] = ok ? x4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
-            for (int u = 0; u < CH; u++) {
-                if (XLDS) {
-                    const int c = base + lane + 64 * u;
-                    const bool ok = c < nch;
-                    xa[u] = ok ? xs4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    xb[u] = ok ? xs4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
+            for (int u = 0; u < CH; u++)
 #pragma unroll
                 for (int j = 0; j < NA; j++) acc[j] += dot8(w[j][u], xa[u], xb[u]);
-            }
         }
     } else {
-        for (int k = lane; k < K; k += 64) {
+        const int kbeg = KS ? wave * 64 : 0, kstep = KS ? 64 * NW : 64;
+        for (int k = kbeg + lane; k < K; k += kstep) {
             const float xv = x[k];
 #pragma unroll
             for (int j = 0; j < NA; j++) acc[j] = fmaf(bf16f(rows[j][k]), xv, acc[j]);
         }
     }
-    if (GEGLU) {
-        const float g = wave_sum(acc[0]), u = wave_sum(acc[1]);
-        if (lane == 0 && r0 < M) a.y[0][r0] = gelu_tanh(g) * u;
-    } else {
+    float tot[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) tot[j] = wave_sum(acc[j]);
+    if (KS) {
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < NA; j++) red[wave][j] = tot[j];
+        }
+        __syncthreads();
+        if (wave != 0) return;
 #pragma unroll
         for (int j = 0; j < NA; j++) {
-            const float s = wave_sum(acc[j]);
-            if (lane == 0 && r0 + j < M) a.y[m][r0 + j] = s;
+            float t = red[0][j];
+#pragma unroll
+            for (int w = 1; w < NW; w++) t += red[w][j];
+            tot[j] = t;
         }
+    }
+    if (lane != 0) return;
+#pragma unroll
+    for (int j = 0; j < RPW; j++) {
+        if (r0 + j >= M) break;
+        a.y[GEGLU ? 0 : m][r0 + j] = GEGLU ? gelu_tanh(tot[j]) * tot[RPW + j] : tot[j];
     }
 }
 
-template <int RPW, int CH, bool VEC, bool XLDS = false, bool GEGLU = false>
+template <int RPW, int CH, bool VEC, bool KS = false, bool GEGLU = false>
 hipError_t launch(const g3k_matvec_args *a, hipStream_t st) {
     int blocks = 0;
     const int nm = GEGLU ? 1 : a->n_mat;
-    for (int m = 0; m < nm; m++) blocks += (a->M[m] + NW * RPW - 1) / (NW * RPW);
-    const size_t lds = XLDS ? (size_t)a->K * sizeof(float) : 0;
-    hipLaunchKernelGGL((matvec_kernel<RPW, CH, VEC, XLDS, GEGLU>), dim3(blocks), dim3(NT), lds, st, *a);
+    const int rows_per_wg = KS ? RPW : NW * RPW;
+    for (int m = 0; m < nm; m++) blocks += (a->M[m] + rows_per_wg - 1) / rows_per_wg;
+    hipLaunchKernelGGL((matvec_kernel<RPW, CH, VEC, KS, GEGLU>), dim3(blocks), dim3(NT), 0, st, *a);
     return hipGetLastError();
 }
 
@@ -187,14 +193,14 @@ extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (a->mode == G3K_MV_GEGLU) {
         if (a->n_mat != 2 || a->M[0] != a->M[1]) return (int)hipErrorInvalidValue;
-        return (int)(vec ? launch<1, 4, true, false, true>(a, st) : launch<1, 1, false, false, true>(a, st));
+        return (int)(vec ? launch<2, 2, true, true, true>(a, st) : launch<2, 1, false, true, true>(a, st));
     }
     if (a->mode != 0) return (int)hipErrorInvalidValue;
     if (!vec) return (int)(rows >= 16384 ? launch<2, 1, false>(a, st) : launch<1, 1, false>(a, st));
     // two rows per wave once there are enough rows to fill the chip with them
     if (rows >= 16384) return (int)launch<2, 8, true>(a, st);
-    // long rows: x in LDS (K floats, at most 64 KiB of the workgroup's LDS)
-    if (a->K >= 8192 && a->K <= G3K_MATVEC_LDS_MAX_K) return (int)launch<1, 4, true, true>(a, st);
-    if (a->K <= 2048) return (int)launch<1, 4, true>(a, st);
+    // long rows: the row's chunks split over the workgroup's waves (5 per lane at K = 10240)
+    if (a->K >= 8192) return (int)launch<2, 5, true, true>(a, st);
+    if (a->K <= 2048) return (int)launch<2, 2, true, true>(a, st);
     return (int)launch<1, 8, true>(a, st);
 }

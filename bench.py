@@ -613,15 +613,16 @@ def main():
 
         def fwd():
             ctx.forward_device(W, 2, pos, logits.data_ptr(), True)
+
         steps = 40
         region, per_call, _ = B.time_calls(ctx, [fwd], steps, 5)
         assert bool(torch.isfinite(logits).all())
         t = region / steps
         extra["forward_token_pos8191"] = {
-            "config": "one token through all 34 layers + final norm + tied logits at pos 8191 "
-                      "(g3attn_forward_device on the uploaded model), Gemma3-4B shapes (hidden 2560, "
-                      "intermediate 10240, vocab 262208), random bf16 weights, cache rows before "
-                      "pos zero",
+            "config": "one token through all 34 layers + final norm + tied logits at pos 8191 on the "
+                      "uploaded model, Gemma3-4B shapes (hidden 2560, intermediate 10240, vocab "
+                      "262208), random bf16 weights, cache rows before pos zero; "
+                      "g3attn_forward_device, device logits",
             "ms_per_token": round(t * 1e3, 3),
             "tokens_per_s": round(1.0 / t, 1),
             "bytes_per_token": fwd_bytes,

@@ -433,9 +433,9 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
     if (tid < 8) {
 #pragma unroll
         for (int w = 1; w < NW; w++) merge_ml(M, L, A, s_m[w][tid], s_l[w][tid], s_a[w][tid]);
-        const float inv = 1.0f / L;
+        // a division, as the single-split path's emit: one split gives the same bits either way
         *reinterpret_cast<float4 *>(p.out + ((size_t)kvh * G + g) * D + d) =
-            make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+            make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
     }
 }
 

@@ -39,7 +39,7 @@ namespace {
 
 using namespace g3k;
 
-constexpr int BM = 128, BN = 128, BK = 32, NT = 256;
+constexpr int BN = 128, BK = 32, NT = 256;
 constexpr int TILE_B = 128 * BK * 2;   // one operand tile in LDS: 8 KiB
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -74,11 +74,10 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// 16 bytes of A.  Plain loads: non-temporal ones stream faster, but the
+// A is read with plain loads: non-temporal ones stream faster, but the
 // decode kernel's measurements showed them returning stale values for memory
 // that a host -> device copy rewrote after kernels had touched it, and A may
 // be re-uploaded in place (g3attn_upload_weights, a caller's own buffers).
-__device__ __forceinline__ uint4 load_a(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
 // NA dot products: RPW consecutive rows of one matrix, or (GEGLU) the same
 // rows of the gate and up matrices.  Without KS each wave owns its own RPW

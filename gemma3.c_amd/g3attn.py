@@ -107,6 +107,7 @@ def lib():
     L.g3attn_forward_token.argtypes = [_vp, C.c_int, C.c_int, C.c_void_p, C.c_int]
     L.g3attn_prefill_tokens.argtypes = [_vp, _i32p, C.c_int, C.c_int, C.c_void_p]
     L.g3attn_matmul_bf16_device.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]
+    L.g3attn_forward_token_device.argtypes = [_vp, C.c_int, C.c_int, _vp]
     L.g3attn_prefill_forward_device.argtypes = [_vp, C.c_void_p, _i32p, C.c_int, C.c_int, _vp]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
@@ -115,7 +116,7 @@ def lib():
                  "g3attn_qkv_proj_device", "g3attn_layer_attention_device",
                  "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
                  "g3attn_prefill_tokens", "g3attn_matmul_bf16_device",
-                 "g3attn_prefill_forward_device"):
+                 "g3attn_prefill_forward_device", "g3attn_forward_token_device"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -350,6 +351,10 @@ class Context:
                                           None if out is None else out.ctypes.data,
                                           int(compute_logits)))
         return out
+
+    def forward_token_device(self, token, pos, logits=None):
+        """The uploaded model's token forward, enqueued; logits: device address or None."""
+        _check(lib().g3attn_forward_token_device(self._h, int(token), int(pos), logits))
 
     def prefill_tokens(self, tokens, start_pos=0, logits=True) -> np.ndarray | None:
         """gemma3_metal_prefill: the last token's logits, or None."""

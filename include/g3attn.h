@@ -242,6 +242,11 @@ const g3attn_weights *g3attn_device_weights(g3attn_ctx *ctx);
  * memory, written when compute_logits and logits are set.  Blocking. */
 int g3attn_forward_token(g3attn_ctx *ctx, int token_id, int pos, float *logits, int compute_logits);
 
+/* g3attn_forward_token with device logits ([vocab_size], may be NULL: no
+ * logits), enqueued on the context stream without waiting, for engines that
+ * sample on the device. */
+int g3attn_forward_token_device(g3attn_ctx *ctx, int token_id, int pos, float *logits);
+
 /* gemma3_metal_prefill (gemma3_metal.m:977-987), gemma3_transformer_
  * prefill_tokens' backend branch (:953-958): tokens[0..n-1] at positions
  * start_pos.. through the uploaded model; logits (host, may be NULL) receives

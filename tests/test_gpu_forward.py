@@ -151,6 +151,39 @@ def test_upload_and_forward_token_match_reference_golden():
     assert np.array_equal(logits, np.stack(dev_rows))
 
 
+def test_forward_token_device_matches_forward_device():
+    """g3attn_forward_token_device (the uploaded model, device logits, no
+    wait) equals g3attn_forward_device of the same token bit for bit, with
+    the two contexts' launches interleaved and only occasional host waits; a
+    re-upload takes effect at the next token."""
+    cfg, f, embed, layers, norm, tokens = MG.forward_case(n=24)
+    HW, keep = G.host_weights(embed, layers, norm)
+    with G.Context(_gpu_config(f), f["max_context"]) as gr, G.Context(_gpu_config(f), f["max_context"]) as eg:
+        gr.upload_weights(HW)
+        W, bufs = _upload(embed, layers, norm)
+        dlg, dle = DeviceBuffer(f["vocab"] * 4), DeviceBuffer(f["vocab"] * 4)
+        for i, t in enumerate(tokens):
+            with_logits = i % 3 != 1                   # tokens without logits in between
+            gr.forward_token_device(int(t), i, dlg.ptr if with_logits else None)
+            eg.forward_device(W, int(t), i, dle.ptr, True)
+            if i % 4 == 0:
+                gr.synchronize()
+            if with_logits:
+                a, b = dlg.download(np.float32, f["vocab"]), dle.download(np.float32, f["vocab"])
+                assert np.array_equal(a, b), i
+        # a new model
+        other = [dict(lw) for lw in layers]
+        other[1]["up_proj"] = MG.weights_bf16(f["inter"], f["hidden"], 0xD1D1)
+        HW2, keep2 = G.host_weights(embed, other, norm)
+        gr.upload_weights(HW2)
+        W2, bufs2 = _upload(embed, other, norm)
+        t = int(tokens[0])
+        gr.forward_token_device(t, len(tokens), dlg.ptr)
+        eg.forward_device(W2, t, len(tokens), dle.ptr, True)
+        assert np.array_equal(dlg.download(np.float32, f["vocab"]), dle.download(np.float32, f["vocab"]))
+    print("[forward_token_device] ok", flush=True)
+
+
 def test_upload_from_a_file_mapping(tmp_path):
     """The loader's case: tensors packed in one mapped file at 2-byte-aligned
     offsets (as in a safetensors blob), uploaded straight from the mapping."""

@@ -65,6 +65,16 @@ def test_config2_global_decode(ctx8k):
     _check(DecodeCase(2, layer=5, pos=8191, max_context=8192), ctx8k, "config2")
 
 
+def test_global_decode_128k():
+    """configs[4]'s global layer at full size: pos 131071 over 131072 cached
+    positions (1 GiB of fp32 K/V; 1024-row splits), against the oracle."""
+    ctx = _ctx(131072, num_layers=6)
+    try:
+        _check(DecodeCase(5, layer=5, pos=131071, max_context=131072), ctx, "128k")
+    finally:
+        ctx.close()
+
+
 @pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 1023])
 def test_short_positions(ctx8k, pos):
     _check(DecodeCase(7, layer=5, pos=pos, max_context=8192), ctx8k, "short-global")

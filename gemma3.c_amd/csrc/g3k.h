@@ -135,6 +135,13 @@ typedef struct {
     int queries_per_wave;     /* 16 (8 waves, 2 per SIMD) or 32 (4 waves, 1 per SIMD) */
     int schedule;             /* 16 queries per wave: 0 = all waves in phase, 1 = SIMD pairs in opposite phase */
     void *ev0, *ev1;          /* hipEvent_t: begin / end of prefill_kernel's dispatch, or NULL */
+    /* Key splits (1, 2 or 4).  With S > 1 every (query block, KV head) runs as
+     * S workgroups over consecutive parts of its key tiles; each writes its
+     * unnormalised O and (max, sum) per query row to part_o [S][n][H_q][D]
+     * and part_ml [S][n][H_q][2], and a second launch merges the S parts
+     * into out (in split order: deterministic). */
+    int ksplit;
+    float *part_o, *part_ml;
 } g3k_prefill_args;
 
 int g3k_prefill(const g3k_prefill_args *a, void *stream);

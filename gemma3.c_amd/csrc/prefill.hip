@@ -329,8 +329,12 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // 1-D grid, longest (latest) query blocks first across all heads: with
     // workgroups dealt round-robin to the 8 XCDs, block id -> (qb, id % H_kv)
     // also keeps each XCD on one KV head (its L2 streams one head's K / V).
+    // with key splits, block id -> (qb, split, kvh), kvh fastest
     const int kvh = blockIdx.x % p.n_kv_heads;
-    const int qb = (int)(gridDim.x / p.n_kv_heads) - 1 - (int)(blockIdx.x / p.n_kv_heads);
+    const int S = p.ksplit;
+    const int pair = (int)(blockIdx.x / p.n_kv_heads);
+    const int split = pair % S;
+    const int qb = (int)(gridDim.x / (p.n_kv_heads * S)) - 1 - pair / S;
     const int qhead = kvh * G + wave / WPH;
     const int tok0 = qb * PB + (wave % WPH) * QW;
     const bool wave_live = tok0 < p.n;
@@ -341,8 +345,13 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // key index range of the workgroup and of this wave (inclusive)
     const int wg_first = p.hist + qb * PB;
     const int wg_last = min(p.hist + min(qb * PB + PB, p.n) - 1, p.nk - 1);
-    const int kt0 = max(0, wg_first - p.window + 1) / BK;
-    const int kt1 = wg_last / BK;
+    int kt0 = max(0, wg_first - p.window + 1) / BK;
+    int kt1 = wg_last / BK;
+    if (S > 1) {   // this split's consecutive part of the tiles (may be empty)
+        const int per = (kt1 - kt0 + S) / S;
+        kt0 += split * per;
+        kt1 = min(kt1, kt0 + per - 1);
+    }
     const int w_first = p.hist + tok0;
     const int w_last = min(w_first + QW - 1, p.hist + p.n - 1);
     const int wkt0 = max(0, w_first - p.window + 1) / BK;
@@ -506,8 +515,25 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         __syncthreads();
     }
 
-    // ---- normalise and write attn_out[token][qhead][dim] ----
+    // ---- normalise and write attn_out[token][qhead][dim], or this split's
+    // unnormalised part ----
     if (!wave_live) return;
+    if (S > 1) {
+        const int hq = p.n_kv_heads * G;
+#pragma unroll
+        for (int b = 0; b < NQB; b++) {
+            const float lt = col4_sum(l_sum[b]);   // all lanes active here
+            const int tok = tok0 + 16 * b + ln;
+            if (tok >= p.n) continue;
+            const size_t row = ((size_t)split * p.n + tok) * hq + qhead;
+            float *po = p.part_o + row * D + 4 * g;
+#pragma unroll
+            for (int mt = 0; mt < 16; mt++)
+                *reinterpret_cast<float4 *>(po + 16 * mt) = make_float4(o[b][mt][0], o[b][mt][1], o[b][mt][2], o[b][mt][3]);
+            if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_ref[b], lt);
+        }
+        return;
+    }
 #pragma unroll
     for (int b = 0; b < NQB; b++) {
         const float inv = 1.0f / col4_sum(l_sum[b]);   // all lanes active here
@@ -532,13 +558,39 @@ __global__ __launch_bounds__(512 / NQB, 1) void prefill_kernel(g3k_prefill_args 
         attend<G, NQB, false>(p, smem);
 }
 
+// Merge of the key splits' parts for one (token, query head) row: one wave,
+// lane t owns dims 4t .. 4t + 3; out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+__global__ __launch_bounds__(64) void prefill_combine_kernel(g3k_prefill_args p) {
+    const size_t row = blockIdx.x, rows = (size_t)p.n * p.n_kv_heads * p.group;
+    const int t = threadIdx.x;
+    float M = NEG_BIG;
+    for (int s = 0; s < p.ksplit; s++) M = fmaxf(M, p.part_ml[(s * rows + row) * 2]);
+    float L = 0.f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < p.ksplit; s++) {
+        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (s * rows + row) * 2);
+        const float f = fast_exp2(ml.x - M);
+        const float4 o = *reinterpret_cast<const float4 *>(p.part_o + (s * rows + row) * D + 4 * t);
+        L += ml.y * f;
+        A.x += o.x * f;
+        A.y += o.y * f;
+        A.z += o.z * f;
+        A.w += o.w * f;
+    }
+    const float inv = 1.0f / L;
+    *reinterpret_cast<float4 *>(p.out + row * D + 4 * t) = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+}
+
 template <int G, int NQB>
 hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
     constexpr int PB = 16 * NQB * ((8 / NQB) / G);
     const int nqb = (a->n + PB - 1) / PB;
     // With timing events the dispatch itself records them (kernel begin / end).
-    hipExtLaunchKernelGGL((prefill_kernel<G, NQB>), dim3(nqb * a->n_kv_heads), dim3(512 / NQB), 0, st,
-                          (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
+    hipExtLaunchKernelGGL((prefill_kernel<G, NQB>), dim3(nqb * a->n_kv_heads * a->ksplit), dim3(512 / NQB), 0,
+                          st, (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a->ksplit == 1) return e;
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3(a->n * a->n_kv_heads * G), dim3(D / 4), 0, st, *a);
     return hipGetLastError();
 }
 
@@ -558,6 +610,8 @@ extern "C" int g3k_prefill(const g3k_prefill_args *a, void *stream) {
     // the 32-bit record count and the fetch offsets
     if (a->ldk % 64 || a->ldk > (1LL << 20) || a->nk > a->ldk || a->hist + a->n != a->nk ||
         a->window < 1 || !a->v_lo_flag)
+        return (int)hipErrorInvalidValue;
+    if ((a->ksplit != 1 && a->ksplit != 2 && a->ksplit != 4) || (a->ksplit > 1 && (!a->part_o || !a->part_ml)))
         return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const bool wide = a->queries_per_wave == 32;

@@ -143,6 +143,7 @@ struct g3attn_ctx {
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
     int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
+    int n_cu;       /* compute units of the device */
 };
 
 static void prof_destroy(g3attn_ctx *c) {
@@ -233,6 +234,9 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
     const char *ov = getenv("G3ATTN_SPLIT_ROWS");
     c->split_rows = ov ? atoi(ov) : 0;
     if (hipGetDevice(&c->device) != hipSuccess) goto fail_rt;
+    if (hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, c->device) != hipSuccess ||
+        c->n_cu < 1)
+        c->n_cu = 256;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) goto fail_rt;
 
     const size_t rope_bytes = (size_t)max_context * D * sizeof(float);
@@ -683,13 +687,26 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     const int hist = start_pos - kstart, nk = hist + n;
     const long long ldk = ((long long)nk + 63) / 64 * 64;
     const size_t v_bytes = align256((size_t)Hkv * ldk * D * sizeof(uint16_t));
+    /* Key splits: when the query blocks x KV heads leave CUs idle (configs[2]:
+     * 32 x 4 = 128 workgroups for 256 CUs, each walking 33 key tiles), every
+     * block's key tiles are split over 2 or 4 workgroups (at least 4 tiles
+     * each) and a small launch merges their parts. */
+    const int pb = 16 * ((c->prefill_qpw == 32 ? 2 : 1)) * ((8 / (c->prefill_qpw == 32 ? 2 : 1)) / c->group);
+    const long long wgs = (long long)((n + pb - 1) / pb) * Hkv;
+    const int tiles = ((nk < W || is_global) ? nk : W + pb) / 32;
+    int S = 1;
+    while (S < 4 && wgs * S < c->n_cu && tiles >= 8 * S) S *= 2;
+    const size_t po_bytes = S > 1 ? align256((size_t)S * n * Hq * D * sizeof(float)) : 0;
+    const size_t pml_bytes = S > 1 ? align256((size_t)S * n * Hq * 2 * sizeof(float)) : 0;
     hipSetDevice(c->device);
-    int rc = grow_pf(c, 4 * v_bytes);
+    int rc = grow_pf(c, 4 * v_bytes + po_bytes + pml_bytes);
     if (rc) return rc;
     unsigned char *ws = (unsigned char *)c->d_pf;
     uint16_t *kq = (uint16_t *)ws;
     uint16_t *vt = (uint16_t *)(ws + 2 * v_bytes);
     uint16_t *vt_lo = (uint16_t *)(ws + 3 * v_bytes);
+    float *part_o = S > 1 ? (float *)(ws + 4 * v_bytes) : NULL;
+    float *part_ml = S > 1 ? (float *)(ws + 4 * v_bytes + po_bytes) : NULL;
     /* a fresh epoch per call: a flag left by an earlier call never matches */
     c->pf_epoch = c->pf_epoch >= INT_MAX - 1 ? 1 : c->pf_epoch + 1;
     const int norm = q_norm && k_norm;
@@ -796,6 +813,9 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
     pa.queries_per_wave = c->prefill_qpw;
     pa.schedule = c->prefill_sched;
+    pa.ksplit = S;
+    pa.part_o = part_o;
+    pa.part_ml = part_ml;
     rc = prof_slot(c, 1, &pa.ev0, &pa.ev1);
     if (rc) return rc;
     rc = g3k_prefill(&pa, c->stream);

@@ -366,8 +366,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by KV head or by sequence, see DESIGN.md, but no multi-GPU "
-              "figure is produced)", file=sys.stderr)
+              "(the path would shard by KV head or by sequence; no multi-GPU figure is "
+              "produced)", file=sys.stderr)
         sys.exit(2)
 
     import torch

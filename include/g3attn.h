@@ -6,9 +6,10 @@
  * attention block that follows the Q/K/V projections: per-head QK-RMSNorm,
  * RoPE from the caller's precomputed table, the KV-cache write and GQA
  * attention (decode: one token; prefill: a causal / sliding-window batch).
- * The surrounding engine (loader, tokenizer, GEMVs, sampler) is untouched; a
+ * The surrounding engine (loader, tokenizer, sampler) is untouched; a
  * transformer built with -DUSE_HIP calls these entry points where the
- * reference runs its CPU attention (hooks: INTEGRATION.md).
+ * reference runs its CPU attention, and optionally the projection, forward
+ * and batched-prefill entry points below for the rest of a token's layers.
  *
  * Conventions kept from the reference:
  *   - 0 on success, a negative gemma3_error code on failure (gemma3.h:57-67):

@@ -347,8 +347,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of sections to run (decode8k = the headline, local512, 128k, "
-                         "stack, gemv, forward, prefill, prefill_local_N2048_w1024, prefill_global_N8192, "
-                         "prefill_global_N8192_fp32_values); default: all")
+                         "stack, gemv, forward, prefill, or one prefill line: prefill_local_N2048_w1024, "
+                         "prefill_global_N8192, prefill_global_N8192_fp32_values, each also with "
+                         "_tiered); default: all")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device-to-device copies of this many MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")

@@ -705,6 +705,47 @@ static int prefill_fast_keys(long long hist, long long n, long long window) {
     return keys >= (double)INT_MAX ? INT_MAX : (int)ceil(keys);
 }
 
+/* Key splits S (1, 2 or 4) of a prefill call.  A workgroup walks the key
+ * tiles of one query block (pb tokens) of one KV head; with S > 1 each
+ * block's tiles are dealt to S workgroups and a second launch merges their
+ * parts.  S minimises a makespan model measured on MI355X:
+ * - a tile step costs ~2.2 us, and a workgroup ~3 us more (query prologue,
+ *   epilogue);
+ * - one workgroup runs per CU (its LDS), and the longest block's part sets a
+ *   floor (a 4096-token global prefill unsplit: 128 tiles on one CU while
+ *   the average is 65);
+ * - the merge moves (S + 1) n H_q 256 floats at ~5 TB/s, plus a launch.
+ * Each split keeps at least 4 tiles. */
+static int prefill_splits(int n, int hist, int nk, int window, int pb, int n_kv, int n_q, int n_cu) {
+    const int nb = (n + pb - 1) / pb;
+    long long total = 0, longest = 0;
+    for (int qb = 0; qb < nb; qb++) {
+        const long long first = (long long)hist + (long long)qb * pb;
+        const long long last = first + pb - 1 < nk - 1 ? first + pb - 1 : nk - 1;
+        const long long k0 = first - window + 1 > 0 ? first - window + 1 : 0;
+        const long long t = last / 32 - k0 / 32 + 1;
+        total += t;
+        if (t > longest) longest = t;
+    }
+    total *= n_kv;
+    const double step_us = 2.2, wg_us = 3.0, merge_bytes_per_us = 5.0e6;
+    int best = 1;
+    double best_us = 0.0;
+    for (int S = 1; S <= 4; S *= 2) {
+        if (S > 1 && longest < 4LL * S) break;
+        const double wgs = (double)nb * n_kv * S;
+        const double floor_us = step_us * (double)((longest + S - 1) / S) + wg_us;
+        const double spread_us = (step_us * (double)total + wg_us * wgs) / (double)(n_cu > 0 ? n_cu : 256);
+        double t = floor_us > spread_us ? floor_us : spread_us;
+        if (S > 1) t += 3.0 + (double)(S + 1) * n * n_q * 256 * 4 / merge_bytes_per_us;
+        if (S == 1 || t < best_us) {
+            best = S;
+            best_us = t;
+        }
+    }
+    return best;
+}
+
 int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
                           const float *K, const float *V, const uint16_t *q_norm,
                           const uint16_t *k_norm, float *attn_out) {
@@ -729,15 +770,8 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     const int hist = start_pos - kstart, nk = hist + n;
     const long long ldk = ((long long)nk + 63) / 64 * 64;
     const size_t v_bytes = align256((size_t)Hkv * ldk * D * sizeof(uint16_t));
-    /* Key splits: when the query blocks x KV heads leave CUs idle (configs[2]:
-     * 32 x 4 = 128 workgroups for 256 CUs, each walking 33 key tiles), every
-     * block's key tiles are split over 2 or 4 workgroups (at least 4 tiles
-     * each) and a small launch merges their parts. */
     const int pb = 16 * ((c->prefill_qpw == 32 ? 2 : 1)) * ((8 / (c->prefill_qpw == 32 ? 2 : 1)) / c->group);
-    const long long wgs = (long long)((n + pb - 1) / pb) * Hkv;
-    const int tiles = ((nk < W || is_global) ? nk : W + pb) / 32;
-    int S = 1;
-    while (S < 4 && wgs * S < c->n_cu && tiles >= 8 * S) S *= 2;
+    const int S = prefill_splits(n, hist, nk, is_global ? INT_MAX / 2 : W, pb, Hkv, Hq, c->n_cu);
     const size_t po_bytes = S > 1 ? align256((size_t)S * n * Hq * D * sizeof(float)) : 0;
     const size_t pml_bytes = S > 1 ? align256((size_t)S * n * Hq * 2 * sizeof(float)) : 0;
     hipSetDevice(c->device);

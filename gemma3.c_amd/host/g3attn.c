@@ -709,8 +709,9 @@ static int prefill_fast_keys(long long hist, long long n, long long window) {
  * tiles of one query block (pb tokens) of one KV head; with S > 1 each
  * block's tiles are dealt to S workgroups and a second launch merges their
  * parts.  S minimises a makespan model measured on MI355X:
- * - a tile step costs ~2.2 us, and a workgroup ~3 us more (query prologue,
- *   epilogue);
+ * - a tile step costs ~2.2 us, and a workgroup ~12 us more: its prologue
+ *   (queries, RoPE rows and the first K / V tiles, read while every CU does
+ *   the same) and its output stores;
  * - one workgroup runs per CU (its LDS), and the longest block's part sets a
  *   floor (a 4096-token global prefill unsplit: 128 tiles on one CU while
  *   the average is 65);
@@ -728,7 +729,7 @@ static int prefill_splits(int n, int hist, int nk, int window, int pb, int n_kv,
         if (t > longest) longest = t;
     }
     total *= n_kv;
-    const double step_us = 2.2, wg_us = 3.0, merge_bytes_per_us = 5.0e6;
+    const double step_us = 2.2, wg_us = 12.0, merge_bytes_per_us = 5.0e6;
     int best = 1;
     double best_us = 0.0;
     for (int S = 1; S <= 4; S *= 2) {

@@ -85,23 +85,6 @@ def measured_traffic(key):
         return None
 
 
-def prefill_passes(n: int, window: int, f32: bool, tiered: bool) -> float:
-    """Issued MFMA work per algorithmic FLOP of a prefill from position 0:
-    exact scores (3 passes) + P_hi, P_lo (+ V_lo) over V = 2.5 (3); a
-    workgroup of 64 query rows whose first row attends at least fast_keys keys
-    scores in one pass (1.5; 2 with V_lo).  fast_keys follows the host's
-    prefill_fast_keys (g3attn.c): 5 n / sum_i 1 / min(i + 1, window)."""
-    exact, one = (3.0, 2.0) if f32 else (2.5, 1.5)
-    if not tiered:
-        return exact
-    i = np.arange(n, dtype=np.float64)
-    keys = np.minimum(i + 1, window)
-    fast = int(np.ceil(5 * n / np.sum(1.0 / keys)))
-    blk_first = np.minimum((i // 64) * 64 + 1, window)
-    w = np.where(blk_first >= fast, one, exact)
-    return float(np.sum(w * keys) / np.sum(keys))
-
-
 def load_binding():
     spec = importlib.util.spec_from_file_location("g3attn", os.path.join(REPO, "gemma3.c_amd", "g3attn.py"))
     mod = importlib.util.module_from_spec(spec)
@@ -348,8 +331,7 @@ def main():
     ap.add_argument("--only", default="",
                     help="comma list of sections to run (decode8k = the headline, local512, 128k, "
                          "stack, gemv, forward, prefill, or one prefill line: prefill_local_N2048_w1024, "
-                         "prefill_global_N8192, prefill_global_N8192_fp32_values, each also with "
-                         "_tiered); default: all")
+                         "prefill_global_N8192, prefill_global_N8192_fp32_values); default: all")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run 5 plain device-to-device copies of this many MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -708,23 +690,16 @@ def main():
     # ---------------- prefill.  The configs' inputs are
     # bf16-valued; the fp32 line feeds values off the bf16 grid, which takes the
     # kernel's extra P_hi.V_lo pass (3x instead of 2.5x the algorithmic MFMA work).
-    # The _tiered lines run G3ATTN_PREFILL_TIERED (one-pass scores on the rows
-    # that attend many keys: 1.5x on those rows).
-    for name, layer, n, window, steps, f32, tiered in (
-            ("prefill_local_N2048_w1024", 0, 2048, 1024, 30, False, False),
-            ("prefill_global_N8192", 5, 8192, 1 << 30, 8, False, False),
-            ("prefill_global_N8192_fp32_values", 5, 8192, 1 << 30, 8, True, False),
-            ("prefill_local_N2048_w1024_tiered", 0, 2048, 1024, 30, False, True),
-            ("prefill_global_N8192_tiered", 5, 8192, 1 << 30, 8, False, True),
-            ("prefill_global_N8192_fp32_values_tiered", 5, 8192, 1 << 30, 8, True, True)):
+    for name, layer, n, window, steps, f32 in (
+            ("prefill_local_N2048_w1024", 0, 2048, 1024, 30, False),
+            ("prefill_global_N8192", 5, 8192, 1 << 30, 8, False),
+            ("prefill_global_N8192_fp32_values", 5, 8192, 1 << 30, 8, True)):
         if only and "prefill" not in only and name not in only:
             continue
         ctx = B.context(8192)
-        if tiered:
-            ctx.set_prefill_precision(G.PREFILL_TIERED)
         gen = B.randn_f32 if f32 else B.randn_bf16
         Q, K, V = gen(n, QS), gen(n, KS), gen(n, KS)
-        passes = prefill_passes(n, window, f32, tiered)
+        passes = 3.0 if f32 else 2.5
         zn16 = torch.zeros(D, dtype=torch.int16, device=B.dev)
         pout = torch.empty(n, QS, device=B.dev, dtype=torch.float32)
         torch.cuda.synchronize()
@@ -743,8 +718,6 @@ def main():
             "kernel_us": round(k_s * 1e6, 1),
             "pairs": prefill_pairs(n, window),
             "algorithmic_GFLOP": round(flops / 1e9, 3),
-            "precision": "tiered" if tiered else "exact",
-            "issued_MFMA_per_algorithmic": round(passes, 3),
             "algorithmic_TFLOP/s_call": round(flops / (region / steps) / 1e12, 1),
             "algorithmic_TFLOP/s_kernel": round(flops / k_s / 1e12, 1),
             "issued_MFMA_TFLOP/s_kernel": round(passes * flops / k_s / 1e12, 1),

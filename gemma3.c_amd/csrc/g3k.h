@@ -142,10 +142,6 @@ typedef struct {
      * into out (in split order: deterministic). */
     int ksplit;
     float *part_o, *part_ml;
-    /* Score tier.  A workgroup whose first query attends at least fast_keys
-     * keys computes q.k in one fp16 MFMA pass (q_hi.k_hi) instead of three;
-     * INT_MAX keeps every workgroup on the three-pass scores. */
-    int fast_keys;
 } g3k_prefill_args;
 
 int g3k_prefill(const g3k_prefill_args *a, void *stream);

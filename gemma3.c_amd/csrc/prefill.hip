@@ -18,12 +18,6 @@
 //             bf16-valued inputs the path is specified on) V_lo is zero and
 //             its pass is skipped, which changes no bit of the result.
 // fp32 accumulation throughout: 2.5x (3x with V_lo) the algorithmic MFMA work.
-// Score tier (fast_keys): a workgroup whose queries all attend at least
-// fast_keys keys scores with the one pass q_hi.k_hi (1.5x the algorithmic
-// work).  The one-pass score error, ~2^-12 relative per product, moves a
-// row's output by up to ~2e-3 of that row's own RMS; the host enables the
-// tier only for rows whose expected output RMS is well below the call's, so
-// the call stays inside the bar.
 //
 // Data flow.  One workgroup = 8 / NQB waves = one KV head x the queries of
 // its G query heads; each wave owns NQB blocks of 16 queries of one head over
@@ -75,12 +69,6 @@ constexpr float NEG_BIG = -1.0e30f;
 constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 #ifndef G3K_KPF
 #define G3K_KPF 1                            // K fragment prefetch depth (d-steps)
-#endif
-#ifndef G3K_KHALF
-#define G3K_KHALF 1                          // one-pass workgroups fetch K hi only
-#endif
-#ifndef G3K_KPF_ONE
-#define G3K_KPF_ONE 3                        // the same for one-pass scores
 #endif
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -191,12 +179,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, un
 }
 
 // K tile kt -> LDS ring slot `dst`: 32 rows of 1 KiB (hi | lo), lane l moves
-// bytes 16 l .. 16 l + 15 of the row; 32 / NW rows per wave.  HI moves the hi
-// halves only (lanes 0-31).
-template <int NW, bool HI>
+// bytes 16 l .. 16 l + 15 of the row; 32 / NW rows per wave.
+template <int NW>
 __device__ __forceinline__ void fetch_k(unsigned char *dst, __amdgpu_buffer_rsrc_t kr, int kt, int wave,
                                         int lane) {
-    if (HI && lane >= 32) return;
 #pragma unroll
     for (int u = 0; u < 32 / NW; u++) {
         const int j = wave * (32 / NW) + u;
@@ -230,24 +216,21 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 
 // S^T of one key tile for this wave's NQB blocks of 16 queries: keys 0-15
 // (s[b][0]) and 16-31 (s[b][1]) of the tile, three fp16 passes (k_hi q_hi,
-// k_hi q_lo, k_lo q_hi), or k_hi q_hi alone when ONE.  Every K fragment read
-// from LDS feeds all NQB query blocks; the fragments of d-step t + 1 are read
-// while step t's MFMAs run.
-template <int NQB, bool ONE>
+// k_hi q_lo, k_lo q_hi).  Every K fragment read from LDS feeds all NQB query
+// blocks; the fragments of d-step t + 1 are read while step t's MFMAs run.
+template <int NQB>
 __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned char *st, int koff0,
                                             int koff1, const half8 (&qh)[NQB][8],
                                             const half8 (&ql)[NQB][8]) {
-    constexpr int PF = ONE ? G3K_KPF_ONE : G3K_KPF;   // d-steps of K fragments in flight
+    constexpr int PF = G3K_KPF;       // d-steps of K fragments in flight
 #pragma unroll
     for (int b = 0; b < NQB; b++) s[b][0] = s[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     half8 f[PF + 1][4];
     auto load = [&](half8 (&r)[4], int t) {
         r[0] = *reinterpret_cast<const half8 *>(st + koff0 + 64 * t);
+        r[1] = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * t);
         r[2] = *reinterpret_cast<const half8 *>(st + koff1 + 64 * t);
-        if (!ONE) {
-            r[1] = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * t);
-            r[3] = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * t);
-        }
+        r[3] = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * t);
     };
 #pragma unroll
     for (int t = 0; t < PF; t++) load(f[t], t);
@@ -260,12 +243,10 @@ __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned c
         for (int b = 0; b < NQB; b++) {
             s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], qh[b][t], s[b][0], 0, 0, 0);
             s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], qh[b][t], s[b][1], 0, 0, 0);
-            if (!ONE) {
-                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], ql[b][t], s[b][0], 0, 0, 0);
-                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], ql[b][t], s[b][1], 0, 0, 0);
-                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][1], qh[b][t], s[b][0], 0, 0, 0);
-                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][3], qh[b][t], s[b][1], 0, 0, 0);
-            }
+            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], ql[b][t], s[b][0], 0, 0, 0);
+            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], ql[b][t], s[b][1], 0, 0, 0);
+            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][1], qh[b][t], s[b][0], 0, 0, 0);
+            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][3], qh[b][t], s[b][1], 0, 0, 0);
         }
         sched_fence();
     }
@@ -331,18 +312,9 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
         }
 }
 
-// Query block of this workgroup (1-D grid, longest (latest) query blocks
-// first across all heads; with key splits, block id -> (qb, split, kvh), kvh
-// fastest).
-__device__ __forceinline__ int block_qb(const g3k_prefill_args &p) {
-    const int pair = (int)(blockIdx.x / p.n_kv_heads);
-    return (int)(gridDim.x / (p.n_kv_heads * p.ksplit)) - 1 - pair / p.ksplit;
-}
-
 // One workgroup's attention: 8 / NQB waves, each owning NQB blocks of 16
-// queries of one head over the full head dim.  VLO adds the P_hi.V_lo pass;
-// ONE scores with one fp16 pass.
-template <int G, int NQB, bool VLO, bool ONE>
+// queries of one head over the full head dim.  VLO adds the P_hi.V_lo pass.
+template <int G, int NQB, bool VLO>
 __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char *smem) {
     constexpr int NW = 8 / NQB;       // waves per workgroup
     constexpr int WPH = NW / G;       // waves per query head
@@ -354,13 +326,15 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // their offsets and LDS addresses in SGPRs (no per-lane loop around each).
     const int fwave = __builtin_amdgcn_readfirstlane(wave);
     const int g = lane >> 4, ln = lane & 15;     // lane group, query column
-    // With workgroups dealt round-robin to the 8 XCDs, block id -> (qb,
-    // id % H_kv) keeps each XCD on one KV head (its L2 streams one head's
-    // K / V).
+    // 1-D grid, longest (latest) query blocks first across all heads: with
+    // workgroups dealt round-robin to the 8 XCDs, block id -> (qb, id % H_kv)
+    // also keeps each XCD on one KV head (its L2 streams one head's K / V).
+    // with key splits, block id -> (qb, split, kvh), kvh fastest
     const int kvh = blockIdx.x % p.n_kv_heads;
     const int S = p.ksplit;
-    const int split = (int)(blockIdx.x / p.n_kv_heads) % S;
-    const int qb = block_qb(p);
+    const int pair = (int)(blockIdx.x / p.n_kv_heads);
+    const int split = pair % S;
+    const int qb = (int)(gridDim.x / (p.n_kv_heads * S)) - 1 - pair / S;
     const int qhead = kvh * G + wave / WPH;
     const int tok0 = qb * PB + (wave % WPH) * QW;
     const bool wave_live = tok0 < p.n;
@@ -398,8 +372,8 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
 
     // ---- K of the first two tiles and V of the first in flight, then this
     // wave's queries ----
-    fetch_k<NW, ONE && G3K_KHALF>(kbuf(kt0), kr, kt0, fwave, lane);
-    if (kt0 + 1 <= kt1) fetch_k<NW, ONE && G3K_KHALF>(kbuf(kt0 + 1), kr, kt0 + 1, fwave, lane);
+    fetch_k<NW>(kbuf(kt0), kr, kt0, fwave, lane);
+    if (kt0 + 1 <= kt1) fetch_k<NW>(kbuf(kt0 + 1), kr, kt0 + 1, fwave, lane);
     fetch_vt(kt0);
 
     half8 qh[NQB][8], ql[NQB][8];
@@ -430,7 +404,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // Software pipeline: iteration kt issues tile kt+1's S^T MFMAs and tile
     // kt's softmax + P.V (in either order, see `late`).
     f32x4 s[NQB][2];
-    if (wave_live && kt0 >= wkt0 && kt0 <= wkt1) tile_scores<NQB, ONE>(s, kbuf(kt0), koff0, koff1, qh, ql);
+    if (wave_live && kt0 >= wkt0 && kt0 <= wkt1) tile_scores<NQB>(s, kbuf(kt0), koff0, koff1, qh, ql);
     // the first iteration refills K tile kt0's slot: every wave must be done
     // reading it
     __syncthreads();
@@ -438,7 +412,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     for (int kt = kt0; kt <= kt1; kt++) {
         // K of tile kt + 2 replaces K of tile kt (scored last iteration), V
         // of tile kt + 1 replaces V of tile kt - 1
-        if (kt + 2 <= kt1) fetch_k<NW, ONE && G3K_KHALF>(kbuf(kt + 2), kr, kt + 2, fwave, lane);
+        if (kt + 2 <= kt1) fetch_k<NW>(kbuf(kt + 2), kr, kt + 2, fwave, lane);
         if (kt + 1 <= kt1) fetch_vt(kt + 1);
         const unsigned char *vs = vbuf(kt);
 
@@ -447,7 +421,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         for (int b = 0; b < NQB; b++) sn[b][0] = s[b][0], sn[b][1] = s[b][1];
         auto scores_next = [&]() {
             if (wave_live && kt + 1 >= wkt0 && kt + 1 <= wkt1)
-                tile_scores<NQB, ONE>(sn, kbuf(kt + 1), koff0, koff1, qh, ql);
+                tile_scores<NQB>(sn, kbuf(kt + 1), koff0, koff1, qh, ql);
         };
         auto softmax_pv = [&]() {
           if (wave_live && kt >= wkt0 && kt <= wkt1) {
@@ -574,22 +548,14 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
 }
 
 // The V_lo pass is taken when this call's staging found a V that is not
-// exactly bf16 (flag == epoch); the branch is uniform over the grid.  The
-// score tier is uniform per workgroup: its first query attends the fewest
-// keys, min(key index + 1, window).
+// exactly bf16 (flag == epoch); the branch is uniform over the grid.
 template <int G, int NQB>
 __global__ __launch_bounds__(512 / NQB, 1) void prefill_kernel(g3k_prefill_args p) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
-    constexpr int PB = 16 * NQB * ((8 / NQB) / G);
-    const int first_keys = min(p.hist + block_qb(p) * PB + 1, p.window);
-    const bool one = first_keys >= p.fast_keys;
-    if (*p.v_lo_flag == p.epoch) {
-        if (one) attend<G, NQB, true, true>(p, smem);
-        else attend<G, NQB, true, false>(p, smem);
-    } else {
-        if (one) attend<G, NQB, false, true>(p, smem);
-        else attend<G, NQB, false, false>(p, smem);
-    }
+    if (*p.v_lo_flag == p.epoch)
+        attend<G, NQB, true>(p, smem);
+    else
+        attend<G, NQB, false>(p, smem);
 }
 
 // Merge of the key splits' parts for one (token, query head) row: one wave,

@@ -26,8 +26,6 @@ OK = 0
 ERR_INVALID_ARG = -1
 ERR_OUT_OF_MEMORY = -4
 ERR_CONTEXT_OVERFLOW = -8
-PREFILL_EXACT = 0    # G3ATTN_PREFILL_EXACT
-PREFILL_TIERED = 1   # G3ATTN_PREFILL_TIERED
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
@@ -111,7 +109,6 @@ def lib():
     L.g3attn_matmul_bf16_device.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]
     L.g3attn_forward_token_device.argtypes = [_vp, C.c_int, C.c_int, _vp]
     L.g3attn_prefill_forward_device.argtypes = [_vp, C.c_void_p, _i32p, C.c_int, C.c_int, _vp]
-    L.g3attn_set_prefill_precision.argtypes = [_vp, C.c_int]
     for name in ("g3attn_decode", "g3attn_prefill", "g3attn_decode_device",
                  "g3attn_prefill_device", "g3attn_kv_append", "g3attn_kv_append_device",
                  "g3attn_kv_write", "g3attn_kv_read", "g3attn_synchronize",
@@ -119,8 +116,7 @@ def lib():
                  "g3attn_qkv_proj_device", "g3attn_layer_attention_device",
                  "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
                  "g3attn_prefill_tokens", "g3attn_matmul_bf16_device",
-                 "g3attn_prefill_forward_device", "g3attn_forward_token_device",
-                 "g3attn_set_prefill_precision"):
+                 "g3attn_prefill_forward_device", "g3attn_forward_token_device"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -284,11 +280,6 @@ class Context:
 
     def synchronize(self):
         _check(lib().g3attn_synchronize(self._h))
-
-    def set_prefill_precision(self, mode: int):
-        """PREFILL_EXACT (default) or PREFILL_TIERED (one-pass scores on the rows
-        of a call that attend many keys relative to its other rows)."""
-        _check(lib().g3attn_set_prefill_precision(self._h, int(mode)))
 
     def profile(self, enable: bool = True):
         """Bracket the main attention kernel of every call with HIP events."""

@@ -142,7 +142,6 @@ struct g3attn_ctx {
     int min_rows;   /* smallest heuristic split */
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
     int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
-    int prefill_precision; /* G3ATTN_PREFILL_EXACT / _TIERED */
     int target_wgs; /* decode workgroups per call (all KV heads) */
     int n_cu;       /* compute units of the device */
 };
@@ -664,47 +663,6 @@ static int grow_pf(g3attn_ctx *c, size_t bytes) {
     return G3_OK;
 }
 
-int g3attn_set_prefill_precision(g3attn_ctx *c, int mode) {
-    if (!c || (mode != G3ATTN_PREFILL_EXACT && mode != G3ATTN_PREFILL_TIERED)) {
-        set_err("g3attn_set_prefill_precision: unknown mode %d", mode);
-        return G3_ERR_INVALID_ARG;
-    }
-    c->prefill_precision = mode;
-    return G3_OK;
-}
-
-/* 1/1 + 1/2 + ... + 1/m (m >= 0): exact below 64, else the asymptotic series
- * ln m + gamma + 1/(2m) - 1/(12m^2) (error < 1/(120 m^4)). */
-static double harmonic(long long m) {
-    if (m < 64) {
-        double h = 0.0;
-        for (long long k = m; k >= 1; k--) h += 1.0 / (double)k;
-        return h;
-    }
-    const double x = (double)m;
-    return log(x) + 0.57721566490153286 + 0.5 / x - 1.0 / (12.0 * x * x);
-}
-
-/* Key count from which a prefill workgroup may score with one fp16 pass
- * (G3ATTN_PREFILL_TIERED).  Token i of the call attends k_i = min(hist + i + 1,
- * window) keys.  The one-pass error of a row is up to ~3e-3 of that row's
- * output RMS, and for weakly peaked attention a row's mean-square output is
- * ~c / k_i, while the bar is 2e-3 of the call's RMS, whose square is ~c times
- * the mean of 1 / k_i.  Rows with 1 / k_i <= mean(1 / k_i) / 5 (RMS at most
- * 0.45 of the call's) take the one pass. */
-static int prefill_fast_keys(long long hist, long long n, long long window) {
-    const long long a = hist + 1, b = hist + n;   /* k_i before the window caps it */
-    double inv = 0.0;
-    if (a < window) {
-        const long long top = b < window - 1 ? b : window - 1;
-        inv += harmonic(top) - harmonic(a - 1);
-    }
-    const long long capped = b >= window ? b - (a > window ? a : window) + 1 : 0;
-    inv += (double)capped / (double)window;
-    const double keys = 5.0 * (double)n / inv;
-    return keys >= (double)INT_MAX ? INT_MAX : (int)ceil(keys);
-}
-
 /* Key splits S (1, 2 or 4) of a prefill call.  A workgroup walks the key
  * tiles of one query block (pb tokens) of one KV head; with S > 1 each
  * block's tiles are dealt to S workgroups and a second launch merges their
@@ -893,9 +851,6 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.ksplit = S;
     pa.part_o = part_o;
     pa.part_ml = part_ml;
-    pa.fast_keys = c->prefill_precision == G3ATTN_PREFILL_TIERED
-                       ? prefill_fast_keys(hist, n, is_global ? INT_MAX / 2 : W)
-                       : INT_MAX;
     rc = prof_slot(c, 1, &pa.ev0, &pa.ev1);
     if (rc) return rc;
     rc = g3k_prefill(&pa, c->stream);

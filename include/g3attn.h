@@ -118,17 +118,6 @@ int g3attn_prefill_device(g3attn_ctx *ctx, int layer, int start_pos, int n,
                           const float *Q, const float *K, const float *V,
                           const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out);
 
-/* Score precision of the prefill (no counterpart in the reference, whose
- * attention is fp32 throughout).  EXACT (the default) splits every MFMA
- * operand so that any input stays within ~2e-5 of the output RMS.  TIERED
- * scores the rows of a call that attend many keys, relative to the call's
- * other rows, with one fp16 pass (error up to ~2e-3 of such a row's own
- * output RMS): on weakly peaked attention, as in the N(0, 1) benchmark
- * shapes, the call stays within 2e-3 of its output RMS.  A chunk whose rows
- * attend similar key counts has no such rows and runs exactly. */
-enum { G3ATTN_PREFILL_EXACT = 0, G3ATTN_PREFILL_TIERED = 1 };
-int g3attn_set_prefill_precision(g3attn_ctx *ctx, int mode);
-
 /* K-norm + RoPE + cache_kv for n tokens without attention: the key/value half
  * of the prefill loop (gemma3_transformer.c:650-671).  K, V [n][num_kv_heads*256]
  * pre-norm (host / device pointers respectively). */

@@ -110,7 +110,9 @@ def _check_cache(ctx, case, Kc, Vc, n_probe=24):
         assert np.array_equal(v[0], Vc[slot]), p
 
 
-def _run(ctx, case, label, full=True):
+def _run(ctx, case, label):
+    """GPU prefill against the oracle (every row) and the cache rows it wrote;
+    returns the error."""
     got = case.gpu(ctx)
     assert got.shape == (case.n, case.qs)
     assert np.all(np.isfinite(got))
@@ -149,6 +151,13 @@ def test_config4_global_prefill(ctx8k):
         dec = ctx8k.decode(case.layer, i, q, k, v, case.norm, case.norm)
         e = float(np.max(np.abs(dec - got[i]))) / rms
         assert e <= TOL, (i, e)
+
+
+@pytest.mark.parametrize("n", [2048, 3000, 4096])
+def test_global_split_shapes(ctx8k, n):
+    """Mid-size global prefills, every row: the host's split model runs them
+    with 4, 2 and 2 key splits (the longest blocks set the makespan unsplit)."""
+    _run(ctx8k, PrefillCase(40 + n, layer=11, start_pos=0, n=n), f"global-{n}")
 
 
 @pytest.mark.parametrize("n", [1, 2, 31, 32, 33, 63, 64, 65, 127, 129, 300])
@@ -265,99 +274,3 @@ def test_prefill_errors(ctx8k):
     assert e.value.rc == G.ERR_INVALID_ARG
     out = ctx8k.prefill(5, 0, Q[:0], K[:0], K[:0])
     assert out.shape == (0, 2048)
-
-
-# ---- G3ATTN_PREFILL_TIERED: one-pass fp16 scores on rows that attend many keys ----
-
-PB = 64   # query positions per prefill workgroup at group 2, 16 queries per wave
-
-
-def _fast_keys(hist, n, window):
-    """Smallest key count scored in one pass: rows whose 1 / k is at most a
-    fifth of the call's mean 1 / k (the host's rule)."""
-    k = np.minimum(hist + np.arange(n, dtype=np.float64) + 1, window)
-    return int(np.ceil(5 * n / np.sum(1.0 / k)))
-
-
-class _Tiered:
-    def __init__(self, ctx):
-        self.ctx = ctx
-
-    def __enter__(self):
-        self.ctx.set_prefill_precision(G.PREFILL_TIERED)
-        return self.ctx
-
-    def __exit__(self, *exc):
-        self.ctx.set_prefill_precision(G.PREFILL_EXACT)
-
-
-def test_tiered_config4(ctx8k):
-    """configs[3] under the tiered policy, every row against the oracle; the
-    exact-tier blocks are bit-identical to the exact policy and the one-pass
-    blocks are not."""
-    case = PrefillCase(4, layer=5, start_pos=0, n=8192)
-    exact = case.gpu(ctx8k)
-    with _Tiered(ctx8k):
-        got = case.gpu(ctx8k)
-    assert np.all(np.isfinite(got))
-    thr = _fast_keys(0, 8192, 1 << 30)
-    split = -(-(thr - 1) // PB) * PB        # first row of the first one-pass block
-    assert 4096 < split < 4608, split
-    assert np.array_equal(got[:split], exact[:split])
-    assert not np.array_equal(got[split:split + PB], exact[split:split + PB])
-    want, _, _ = case.oracle()
-    err = rel_err(got, want)
-    err_x = rel_err(exact, want)
-    print(f"[tiered config4] fast_keys={thr} one-pass rows {split}.. every row: rel_err={err:.3e} "
-          f"(exact policy {err_x:.3e})", flush=True)
-    assert err <= TOL, err
-    # the exact policy's own distance (~1e-4 here) is the two sides' fp32
-    # summation orders over up to 8192 keys; the one pass adds several times that
-    assert err > 3 * err_x
-
-
-def test_tiered_config3_local(ctx8k):
-    """configs[2] (window 1024): the capped rows' RMS is ~0.55 of the call's,
-    above the rule's 0.45, so no row takes the one pass."""
-    assert _fast_keys(0, 2048, 1024) > 1024
-    case = PrefillCase(3, layer=0, start_pos=0, n=2048)
-    exact = case.gpu(ctx8k)
-    with _Tiered(ctx8k):
-        got = case.gpu(ctx8k)
-    assert np.array_equal(got, exact)
-
-
-def test_tiered_global_4096(ctx8k):
-    """A 4096-token global prefill under the tiered policy, every row against the oracle."""
-    with _Tiered(ctx8k):
-        err = _run(ctx8k, PrefillCase(72, layer=11, start_pos=0, n=4096), "tiered-4096")
-    assert err > 1e-4          # the one-pass tier ran
-
-
-@pytest.mark.parametrize("layer,n", [(5, 1500), (11, 3000)])
-def test_tiered_fp32_values(ctx8k, layer, n):
-    """Off-grid q, k and v (the P_hi.V_lo pass with one-pass scores)."""
-    case = PrefillCase(70 + layer, layer=layer, start_pos=0, n=n)
-    case.Q, case.K, case.V = _off_grid(case.Q), _off_grid(case.K), _off_grid(case.V)
-    with _Tiered(ctx8k):
-        _run(ctx8k, case, f"tiered-fp32-{layer}")
-
-
-@pytest.mark.parametrize("layer,start,n", [(5, 4096, 2048), (3, 1500, 1200), (11, 300, 400)])
-def test_tiered_chunk_without_fast_rows(ctx8k, layer, start, n):
-    """A chunk whose rows attend similar key counts has no one-pass rows: the
-    tiered policy returns the exact policy's bits."""
-    window = 1 << 30 if O.is_global_layer(layer) else 1024
-    hist = start if O.is_global_layer(layer) else min(start, window - 1)
-    assert _fast_keys(hist, n, window) > min(hist + n, window)
-    case = PrefillCase(80 + layer, layer=layer, start_pos=start, n=n)
-    exact = case.gpu(ctx8k)
-    with _Tiered(ctx8k):
-        got = case.gpu(ctx8k)
-    assert np.array_equal(got, exact)
-
-
-def test_prefill_precision_errors(ctx8k):
-    with pytest.raises(G.G3AttnError) as e:
-        ctx8k.set_prefill_precision(2)
-    assert e.value.rc == G.ERR_INVALID_ARG

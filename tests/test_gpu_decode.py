@@ -65,6 +65,24 @@ def test_config2_global_decode(ctx8k):
     _check(DecodeCase(2, layer=5, pos=8191, max_context=8192), ctx8k, "config2")
 
 
+@pytest.mark.timeout(600)   # ~1 minute, mostly the host building 5 GiB of seeded history
+def test_config5_stack_128k():
+    """configs[4] in full: one decode step at pos 131071 through all 34 layers
+    of one context (29 local layers over their 1024-slot rings, 5 global
+    layers over 131072 cached positions, 5 GiB of fp32 K/V), each layer with
+    its own data, against the oracle."""
+    ctx = _ctx(131072)
+    try:
+        worst = 0.0
+        for layer in range(34):
+            case = DecodeCase(5, layer=layer, pos=131071, max_context=131072, layer_seed=layer + 1)
+            worst = max(worst, _check(case, ctx, f"stack-{layer}"))
+            del case
+        print(f"[stack128k] 34 layers, worst rel_err={worst:.3e}", flush=True)
+    finally:
+        ctx.close()
+
+
 def test_global_decode_128k():
     """configs[4]'s global layer at full size: pos 131071 over 131072 cached
     positions (1 GiB of fp32 K/V; 1024-row splits), against the oracle."""

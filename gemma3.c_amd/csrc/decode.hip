@@ -39,11 +39,11 @@ constexpr int D = G3K_HEAD_DIM;
 constexpr int NT = 256;               // threads per workgroup
 constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
-// one row so its larger q / acc arrays fit without spills.
-#ifndef G3K_DEC_R
-#define G3K_DEC_R 2
-#endif
-template <int G> constexpr int rows_for() { return G >= 4 ? 1 : G3K_DEC_R; }
+// one row so its larger q / acc arrays fit without spills.  R = 4 (one
+// 64-row step per workgroup at 8K, with q moved to LDS to fit 256 VGPRs)
+// was built and returned wrong outputs on the GPU in spilling and
+// non-spilling builds alike; only the R values below are tested.
+template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
 // in flight per wave, one contiguous row range per split.  Double-buffered

@@ -40,9 +40,11 @@ constexpr int NT = 256;               // threads per workgroup
 constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
 // one row so its larger q / acc arrays fit without spills.  R = 4 (one
-// 64-row step per workgroup at 8K, with q moved to LDS to fit 256 VGPRs)
-// was built and returned wrong outputs on the GPU in spilling and
-// non-spilling builds alike; only the R values below are tested.
+// 64-row step per workgroup at 8K) was built: its -O3 builds (spilling, or
+// with q moved to LDS to fit 256 VGPRs) returned wrong outputs, its -O1
+// build correct ones 40% slower, so the cause is in how -O3 compiles that
+// variant, not in the R-generic indexing.  Only the R values below are built
+// and tested.
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step

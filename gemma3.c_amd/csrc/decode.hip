@@ -27,6 +27,7 @@
 //   back the XCD's whole L2: measured slower than the extra launch.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+#include <pthread.h>
 
 #include "g3k.h"
 #include "g3k_device.h"
@@ -475,6 +476,43 @@ extern "C" int g3k_decode(const g3k_decode_args *a, int fused, void *stream) {
         case 4: return (int)(fused ? launch<4, true>(a, st) : launch<4, false>(a, st));
         default: return (int)hipErrorInvalidValue;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Fixed scratch of the allocation-free gemma3_gqa entry point: the split
+// partials of up to G3K_NOALLOC_MAX_HEADS query heads x G3K_MAX_SPLITS splits
+// (acc [.][D], then (max, sum) [.][2]), 4.03 MiB per device, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel: that
+// name is a host-side stand-in, not a device address.  Each device's address
+// comes from hipGetSymbolAddress, once per device with that device current.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t NOALLOC_ACC = (size_t)G3K_NOALLOC_MAX_HEADS * G3K_MAX_SPLITS * D;
+constexpr size_t NOALLOC_ML = (size_t)G3K_NOALLOC_MAX_HEADS * G3K_MAX_SPLITS * 2;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+float *g_scratch_ptr[NOALLOC_MAX_DEVICES];
+pthread_mutex_t g_scratch_lock = PTHREAD_MUTEX_INITIALIZER;
+}  // namespace
+
+static __device__ __align__(256) float scratch[NOALLOC_ACC + NOALLOC_ML];
+
+extern "C" int g3k_noalloc_scratch(float **acc, float **ml) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    pthread_mutex_lock(&g_scratch_lock);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) g_scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    float *base = g_scratch_ptr[dev];
+    pthread_mutex_unlock(&g_scratch_lock);
+    if (!base) return (int)(e != hipSuccess ? e : hipErrorInvalidSymbol);
+    *acc = base;
+    *ml = base + NOALLOC_ACC;
+    return 0;
 }
 
 extern "C" int g3k_decode_capacity(int group, int fused) {

@@ -61,6 +61,14 @@ int g3k_decode(const g3k_decode_args *a, int fused, void *stream);
  * current device (occupancy x compute units); 0 if unknown. */
 int g3k_decode_capacity(int group, int fused);
 
+/* The current device's fixed split-partial scratch of the allocation-free
+ * gqa entry point (a static device array; its address is looked up once per
+ * device).  acc holds G3K_NOALLOC_MAX_HEADS * G3K_MAX_SPLITS * head_dim
+ * floats in the ws_acc layout of g3k_decode_args, ml the matching (max, sum)
+ * pairs.  Allocates nothing. */
+#define G3K_NOALLOC_MAX_HEADS 16
+int g3k_noalloc_scratch(float **acc, float **ml);
+
 /* Batched QK-norm + RoPE + cache write for n tokens (positions start_pos..).
  *   Q [n][H_q][D] (may be NULL) -> q_out head-major [H_q][n][D];
  *   K, V [n][H_kv][D] -> k_dst/v_dst rows: slot = ring ? (pos % ring) : (pos - dst_pos0),

@@ -88,6 +88,8 @@ def lib():
     L.g3attn_gqa.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
                              C.c_float, _vp, _vp]
     L.g3attn_gqa.restype = None
+    L.g3attn_gqa_noalloc.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                     C.c_float, _vp, _vp]
     L.g3attn_stream.argtypes = [_vp]
     L.g3attn_stream.restype = _vp
     L.g3attn_synchronize.argtypes = [_vp]
@@ -116,7 +118,8 @@ def lib():
                  "g3attn_qkv_proj_device", "g3attn_layer_attention_device",
                  "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
                  "g3attn_prefill_tokens", "g3attn_matmul_bf16_device",
-                 "g3attn_prefill_forward_device", "g3attn_forward_token_device"):
+                 "g3attn_prefill_forward_device", "g3attn_forward_token_device",
+                 "g3attn_gqa_noalloc"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -166,6 +169,13 @@ def gqa(q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim=256, scale=0
     if err:
         raise G3AttnError(ERR_INVALID_ARG, err)
     return out
+
+
+def gqa_noalloc(out_ptr, q_ptr, k_ptr, v_ptr, n_heads, n_kv_heads, seq_len, head_dim=256,
+                scale=0.0625, mask_ptr=None, stream=None) -> None:
+    """g3attn_gqa_noalloc on device addresses (ints); enqueues and returns."""
+    _check(lib().g3attn_gqa_noalloc(out_ptr, q_ptr, k_ptr, v_ptr, n_heads, n_kv_heads, seq_len,
+                                    head_dim, scale, mask_ptr, stream))
 
 
 def matvec_bf16(A, x) -> np.ndarray:

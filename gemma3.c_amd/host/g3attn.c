@@ -25,6 +25,7 @@
 #define G3_ERR_CONTEXT_OVERFLOW (-8)
 
 #define LOG2E 1.4426950408889634f
+_Static_assert(G3ATTN_NOALLOC_MAX_HEADS == G3K_NOALLOC_MAX_HEADS, "fixed scratch size");
 #define G3_PROF_CAP 256
 #define D G3K_HEAD_DIM
 
@@ -1711,18 +1712,50 @@ static int gqa_init(void) {
     return G3_OK;
 }
 
-static int gqa_run(float *output, const float *q, const float *k_cache, const float *v_cache,
-                   int n_heads, int n_kv, int seq_len, int head_dim, float scale, const float *mask) {
+/* The gemma3_gqa call on device buffers: q [n_heads][D], K/V rows
+ * [seq_len][n_kv][D] (the reference layout), optional additive mask
+ * [seq_len], out [n_heads][D]; split partials in ws_acc / ws_ml. */
+static void gqa_args(g3k_decode_args *a, float *dout, const float *dq, const float *dk, const float *dv,
+                     const float *dm, int n_heads, int n_kv, int seq_len, float scale, float *ws_acc,
+                     float *ws_ml) {
+    memset(a, 0, sizeof *a);
+    a->q = dq;
+    a->kc = (float *)dk;
+    a->vc = (float *)dv;
+    a->row_stride = (long long)n_kv * D;
+    a->head_stride = D;
+    a->n_stream = seq_len;
+    a->skip = INT_MAX;
+    a->new_slot = -1;
+    a->mask = dm;
+    a->qscale = scale * LOG2E;
+    choose_splits(seq_len, n_kv, 512, 0, 64, a);
+    a->n_kv_heads = n_kv;
+    a->group = n_heads / n_kv;
+    a->out = dout;
+    a->ws_acc = ws_acc;
+    a->ws_ml = ws_ml;
+}
+
+static int gqa_check(const float *output, const float *q, const float *k_cache, const float *v_cache,
+                     int n_heads, int n_kv, int seq_len, int head_dim, const char *who) {
     if (!output || !q || !k_cache || !v_cache || seq_len <= 0) {
-        set_err("g3attn_gqa: null buffer or seq_len <= 0");
+        set_err("%s: null buffer or seq_len <= 0", who);
         return G3_ERR_INVALID_ARG;
     }
     if (!check_shape(n_heads, n_kv, head_dim)) return G3_ERR_INVALID_ARG;
+    return G3_OK;
+}
+
+static int gqa_run(float *output, const float *q, const float *k_cache, const float *v_cache,
+                   int n_heads, int n_kv, int seq_len, int head_dim, float scale, const float *mask) {
+    int rc = gqa_check(output, q, k_cache, v_cache, n_heads, n_kv, seq_len, head_dim, "g3attn_gqa");
+    if (rc) return rc;
     if (n_kv > GQA_MAX_KV) {
         set_err("g3attn_gqa: n_kv_heads %d > %d", n_kv, GQA_MAX_KV);
         return G3_ERR_INVALID_ARG;
     }
-    int rc = gqa_init();
+    rc = gqa_init();
     if (rc) return rc;
     hipSetDevice(g_gqa.device);
     const size_t qs = (size_t)n_heads * D, kvb = (size_t)seq_len * n_kv * D * sizeof(float);
@@ -1744,23 +1777,7 @@ static int gqa_run(float *output, const float *q, const float *k_cache, const fl
     HIP_TRY(hipMemcpyAsync(dv, v_cache, kvb, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
     if (mask) HIP_TRY(hipMemcpyAsync(dm, mask, (size_t)seq_len * 4, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
     g3k_decode_args a;
-    memset(&a, 0, sizeof a);
-    a.q = dq;
-    a.kc = dk;
-    a.vc = dv;
-    a.row_stride = (long long)n_kv * D;
-    a.head_stride = D;
-    a.n_stream = seq_len;
-    a.skip = INT_MAX;
-    a.new_slot = -1;
-    a.mask = dm;
-    a.qscale = scale * LOG2E;
-    choose_splits(seq_len, n_kv, 512, 0, 64, &a);
-    a.n_kv_heads = n_kv;
-    a.group = n_heads / n_kv;
-    a.out = dout;
-    a.ws_acc = g_gqa.ws_acc;
-    a.ws_ml = g_gqa.ws_ml;
+    gqa_args(&a, dout, dq, dk, dv, dm, n_heads, n_kv, seq_len, scale, g_gqa.ws_acc, g_gqa.ws_ml);
     rc = g3k_decode(&a, 0, s);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa launch");
     HIP_TRY(hipMemcpyAsync(output, dout, qs * 4, hipMemcpyDeviceToHost, s), "g3attn_gqa download");
@@ -1777,6 +1794,33 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
     gqa_run(output, q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim, scale, mask);
     pthread_mutex_unlock(&g_gqa.lock);
 }
+
+/* The same computation on device buffers with no allocation at all: the
+ * split partials go to the library's fixed static device scratch (see
+ * g3k_noalloc_scratch), looked up once per device.  Same split choice as
+ * g3attn_gqa, so the two agree bit for bit. */
+int g3attn_gqa_noalloc(float *output, const float *q, const float *k_cache, const float *v_cache,
+                       int n_heads, int n_kv_heads, int seq_len, int head_dim, float scale,
+                       const float *mask, void *stream) {
+    g_err[0] = 0;
+    int rc = gqa_check(output, q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim,
+                       "g3attn_gqa_noalloc");
+    if (rc) return rc;
+    if (n_heads > G3ATTN_NOALLOC_MAX_HEADS) {
+        set_err("g3attn_gqa_noalloc: n_heads %d exceeds the fixed scratch's %d heads", n_heads,
+                G3ATTN_NOALLOC_MAX_HEADS);
+        return G3_ERR_INVALID_ARG;
+    }
+    float *acc = NULL, *ml = NULL;
+    rc = g3k_noalloc_scratch(&acc, &ml);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa_noalloc scratch");
+    g3k_decode_args a;
+    gqa_args(&a, output, q, k_cache, v_cache, mask, n_heads, n_kv_heads, seq_len, scale, acc, ml);
+    rc = g3k_decode(&a, 0, stream);
+    if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa_noalloc launch");
+    return G3_OK;
+}
+
 
 /* Host-pointer GEMV through the same process-wide stream; its own grow-on-
  * demand device buffer holds A, x and y. */

@@ -145,6 +145,23 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
                 int n_heads, int n_kv_heads, int seq_len, int head_dim,
                 float scale, const float *mask, float *scores_buf);
 
+/* Allocation-free variant of g3attn_gqa.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Every
+ * pointer is a DEVICE buffer with g3attn_gqa's shapes (q [n_heads][head_dim],
+ * K/V [seq_len][n_kv_heads][head_dim], mask [seq_len] or NULL, output
+ * [n_heads][head_dim]); the launch goes on `stream` (a hipStream_t, NULL =
+ * the null stream) and the call returns without waiting.  The split partials
+ * live in a fixed static device scratch of 4.03 MiB per device, held until
+ * the process ends, so n_heads <= G3ATTN_NOALLOC_MAX_HEADS (larger calls
+ * return -1 with a message).  Calls that overlap on one GPU (other streams,
+ * other threads) race on that scratch; serialise them.  Same splits and
+ * kernels as g3attn_gqa: the results agree bit for bit.  Returns 0 or -1. */
+#define G3ATTN_NOALLOC_MAX_HEADS 16
+int g3attn_gqa_noalloc(float *output, const float *q, const float *k_cache, const float *v_cache,
+                       int n_heads, int n_kv_heads, int seq_len, int head_dim, float scale,
+                       const float *mask, void *stream);
+
 /* y [M] = A [M][K] . x [K] with A bf16 row-major and fp32 x, y: the same
  * signature and arithmetic as gemma3_matvec_bf16 (gemma3_kernels.h:217-218,
  * gemma3_kernels.c:188-238; fp32 accumulation, summation order differs).

@@ -118,11 +118,14 @@ class DecodeCase:
     """
 
     def __init__(self, config: int, layer: int, pos: int, max_context: int,
-                 window: int = 1024, norm: bool = True, layer_seed: int = 0):
+                 window: int = 1024, norm: bool = True, layer_seed: int = 0,
+                 n_heads: int = HQ, n_kv: int = HKV):
         self.config, self.layer, self.pos = config, layer, pos
-        self.cfg = O.Config(max_context=max_context, sliding_window=window)
+        self.cfg = O.Config(max_context=max_context, sliding_window=window, num_heads=n_heads,
+                            num_kv_heads=n_kv)
         self.is_global = O.is_global_layer(layer)
         self.table = O.rope_table(max_context, self.cfg.theta(layer))
+        QS, KS, HKV = n_heads * D, n_kv * D, n_kv
         self.q = tensor(config, 1, QS, layer=layer_seed)
         # oldest position still visible to the new token (ring keeps `window` slots)
         self.lo = 0 if self.is_global else max(0, pos - window)
@@ -143,8 +146,9 @@ class DecodeCase:
         return p if self.is_global else p % self.cfg.sliding_window
 
     def oracle_cache(self):
-        Kc = np.zeros((self.rows, KS), dtype=np.float32)
-        Vc = np.zeros((self.rows, KS), dtype=np.float32)
+        ks = self.cfg.num_kv_heads * D
+        Kc = np.zeros((self.rows, ks), dtype=np.float32)
+        Vc = np.zeros((self.rows, ks), dtype=np.float32)
         s = self.slots()
         Kc[s] = self.k_rows
         Vc[s] = self.v_hist

@@ -17,8 +17,9 @@ G = g3attn()
 FP32_BAR = 1e-4
 
 
-def _ctx(max_context, window=1024, num_layers=34):
-    cfg = G.default_config(max_context=max_context, sliding_window=window, num_layers=num_layers)
+def _ctx(max_context, window=1024, num_layers=34, n_heads=8, n_kv=4):
+    cfg = G.default_config(max_context=max_context, sliding_window=window, num_layers=num_layers,
+                           num_heads=n_heads, num_kv_heads=n_kv)
     return G.Context(cfg, max_context,
                      O.rope_table(max_context, 10000.0), O.rope_table(max_context, 1e6))
 
@@ -103,6 +104,21 @@ def test_short_positions(ctx8k, pos):
 def test_local_ring_wrap(ctx8k, pos):
     """pos >= window: the ring holds exactly positions pos-1023..pos."""
     _check(DecodeCase(8, layer=0, pos=pos, max_context=8192), ctx8k, "ring")
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(4, 4), (8, 2)])
+def test_decode_gqa_groups(n_heads, n_kv):
+    """The fused decode at GQA groups 1 and 4 (the configs use 2): a local
+    layer inside the window and across the ring wrap, a global layer, with
+    and without QK-norm."""
+    ctx = _ctx(4096, num_layers=6, n_heads=n_heads, n_kv=n_kv)
+    try:
+        for layer, pos, norm in ((0, 700, True), (1, 2500, True), (5, 3000, True), (5, 999, False)):
+            case = DecodeCase(12, layer=layer, pos=pos, max_context=4096, norm=norm,
+                              n_heads=n_heads, n_kv=n_kv)
+            _check(case, ctx, f"group{n_heads // n_kv}")
+    finally:
+        ctx.close()
 
 
 def test_no_norm(ctx8k):

@@ -22,9 +22,9 @@
 //   Softmax runs in the exp2 domain: q is pre-scaled by scale*log2(e).
 //   Waves merge through LDS; with more than one split each workgroup writes
 //   an (m, l, acc) partial and a second small launch (combine_kernel)
-//   merges them.  A last-arrival combine inside the kernel would need a
-//   device-scope release fence per workgroup, and on gfx950 that writes
-//   back the XCD's whole L2: measured slower than the extra launch.
+//   merges them.  A last-arrival merge inside the kernel (an arrival counter
+//   per KV head, one agent-scope release per workgroup, the last workgroup
+//   merging) was measured no faster for local layers and slower at 8K.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <pthread.h>
@@ -40,12 +40,12 @@ constexpr int D = G3K_HEAD_DIM;
 constexpr int NT = 256;               // threads per workgroup
 constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
-// one row so its larger q / acc arrays fit without spills.  R = 4 (one
-// 64-row step per workgroup at 8K) was built: its -O3 builds (spilling, or
-// with q moved to LDS to fit 256 VGPRs) returned wrong outputs, its -O1
-// build correct ones 40% slower, so the cause is in how -O3 compiles that
-// variant, not in the R-generic indexing.  Only the R values below are built
-// and tested.
+// one row so its larger q / acc arrays fit without spills.  Only the R
+// values below are built and tested.  An R = 4 variant (one 64-row step per
+// workgroup at 8K, with the query moved to LDS to fit 256 VGPRs) returned
+// wrong outputs from its -O3 builds and correct ones, 40% slower, from -O1;
+// the cause was not found (undefined behaviour or a missing wait in that
+// variant's query-in-LDS code is as likely as a compiler fault).
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
@@ -102,28 +102,47 @@ __device__ __forceinline__ void store16(float *dst, const float (&x)[4][4], int 
 }
 
 
-// One cache row's 16 dims of this lane.  Plain loads: non-temporal ones were
-// measured faster (6.75 vs 6.0 TB/s at 128K) but returned stale values for
-// rows that a host -> device copy rewrote after a kernel had read them
-// (tests/test_gpu_decode.py::test_cache_rewritten_by_copy).
+// One cache row's 16 dims of this lane.
 __device__ __forceinline__ void load16_stream(float (&x)[4][4], const float *src, int c) { load16(x, src, c); }
 
-template <int R>
+// The same through a buffer descriptor with the non-temporal cache policy
+// (the context-owned cache: streamed once per call, not worth keeping in
+// L2).  rs covers one KV head's rows; voff = the row's byte offset + 16 c.
+__device__ __forceinline__ void load16_nt(float (&x)[4][4], __amdgpu_buffer_rsrc_t rs, unsigned voff) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float4 t = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 256 * j, 0, 2));
+        x[j][0] = t.x; x[j][1] = t.y; x[j][2] = t.z; x[j][3] = t.w;
+    }
+}
+
+// Buffer descriptor over one KV head's cache rows (bytes < 2^32).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const float *base, long long head_stride) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)(head_stride * 4), 0x00020000);
+}
+
+template <int R, bool NTL>
 __device__ __forceinline__ void load_step(float (&kk)[R][4][4], float (&vv)[R][4][4],
                                           const float *kbase, const float *vbase, long long rs,
-                                          int base, int c1, int skip, int grp, int c) {
+                                          long long head_stride, int base, int c1, int skip, int grp, int c) {
     const int base_row = base + (base >= skip);
+    int rows[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const int idx = base + grp * R + r;
-        const int row = idx < c1 ? idx + (idx >= skip) : base_row;
-        load16_stream(kk[r], kbase + (size_t)row * rs, c);
+        rows[r] = idx < c1 ? idx + (idx >= skip) : base_row;
     }
+    if (NTL) {
+        const __amdgpu_buffer_rsrc_t kr = head_rsrc(kbase, head_stride), vr = head_rsrc(vbase, head_stride);
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int idx = base + grp * R + r;
-        const int row = idx < c1 ? idx + (idx >= skip) : base_row;
-        load16_stream(vv[r], vbase + (size_t)row * rs, c);
+        for (int r = 0; r < R; r++) load16_nt(kk[r], kr, (unsigned)(rows[r] * rs * 4) + 16 * c);
+#pragma unroll
+        for (int r = 0; r < R; r++) load16_nt(vv[r], vr, (unsigned)(rows[r] * rs * 4) + 16 * c);
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) load16_stream(kk[r], kbase + (size_t)rows[r] * rs, c);
+#pragma unroll
+        for (int r = 0; r < R; r++) load16_stream(vv[r], vbase + (size_t)rows[r] * rs, c);
     }
 }
 
@@ -207,7 +226,19 @@ __device__ __forceinline__ void step_compute(const float (&kk)[R][4][4], const f
     }
 }
 
-template <int G, bool FUSED>
+// (M, L, A) <- merge of two online-softmax partials
+__device__ __forceinline__ void merge_ml(float &M, float &L, float4 &A, float m2, float l2, float4 a2) {
+    const float Mn = fmaxf(M, m2);
+    const float f1 = fast_exp2(M - Mn), f2 = fast_exp2(m2 - Mn);
+    L = L * f1 + l2 * f2;
+    A.x = A.x * f1 + a2.x * f2;
+    A.y = A.y * f1 + a2.y * f2;
+    A.z = A.z * f1 + a2.z * f2;
+    A.w = A.w * f1 + a2.w * f2;
+    M = Mn;
+}
+
+template <int G, bool FUSED, bool NTL>
 __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     constexpr int R = rows_for<G>();
     constexpr int ROWS_PER_WAVE_STEP = 4 * R;
@@ -228,7 +259,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     // ---- first step's K/V loads go out before the query prologue ----
     float kk[R][4][4], vv[R][4][4];
     int base = c0 + wave * ROWS_PER_WAVE_STEP;
-    if (base < c1) load_step(kk, vv, kbase, vbase, p.row_stride, base, c1, p.skip, grp, c);
+    if (base < c1) load_step<R, NTL>(kk, vv, kbase, vbase, p.row_stride, p.head_stride, base, c1, p.skip, grp, c);
 
     // ---- query: this lane's 16 dims of each of the G query heads ----
     float qv[G][4][4];
@@ -295,7 +326,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     while (base < c1) {
         step_compute<G, R, FUSED>(kk, vv, qv, m, l, acc, base, c1, grp, p.mask);
         base += stride;
-        if (base < c1) load_step(kk, vv, kbase, vbase, p.row_stride, base, c1, p.skip, grp, c);
+        if (base < c1) load_step<R, NTL>(kk, vv, kbase, vbase, p.row_stride, p.head_stride, base, c1, p.skip, grp, c);
     }
 
     // ---- merge the four lane-groups of each wave (they share m) ----
@@ -349,7 +380,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         emit<G>(s_res, s_resml, out, nullptr, nullptr);
         return;
     }
-    // ---- this split's partial; combine_kernel merges the splits ----
+    // ---- this split's partial ----
     const size_t slot = (size_t)kvh * G3K_MAX_SPLITS + split;
     emit<G>(s_res, s_resml, nullptr, p.ws_acc + slot * G * D, p.ws_ml + slot * G * 2);
 }
@@ -362,18 +393,6 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
 // split lanes of a wave by shuffles and across the 4 waves through LDS.
 constexpr int CMB_SL = NT / 8;                     // split lanes per workgroup
 constexpr int CMB_U = G3K_MAX_SPLITS / CMB_SL;     // splits per thread, at most
-
-// (M, L, A) <- merge of two online-softmax partials
-__device__ __forceinline__ void merge_ml(float &M, float &L, float4 &A, float m2, float l2, float4 a2) {
-    const float Mn = fmaxf(M, m2);
-    const float f1 = fast_exp2(M - Mn), f2 = fast_exp2(m2 - Mn);
-    L = L * f1 + l2 * f2;
-    A.x = A.x * f1 + a2.x * f2;
-    A.y = A.y * f1 + a2.y * f2;
-    A.z = A.z * f1 + a2.z * f2;
-    A.w = A.w * f1 + a2.w * f2;
-    M = Mn;
-}
 
 template <int G>
 __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
@@ -442,11 +461,11 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
     }
 }
 
-template <int G, bool FUSED>
+template <int G, bool FUSED, bool NTL>
 hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
     dim3 grid(a->n_splits, a->n_kv_heads);
     // With timing events the dispatch itself records them (kernel begin / end).
-    hipExtLaunchKernelGGL((decode_kernel<G, FUSED>), grid, dim3(NT), 0, st, (hipEvent_t)a->ev0,
+    hipExtLaunchKernelGGL((decode_kernel<G, FUSED, NTL>), grid, dim3(NT), 0, st, (hipEvent_t)a->ev0,
                           (hipEvent_t)a->ev1, 0, *a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a->n_splits == 1) return e;
@@ -454,11 +473,17 @@ hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int G>
+hipError_t launch_g(const g3k_decode_args *a, int fused, hipStream_t st) {
+    if (!fused) return launch<G, false, false>(a, st);
+    return a->nt_loads ? launch<G, true, true>(a, st) : launch<G, true, false>(a, st);
+}
+
 template <int G, bool FUSED>
 int capacity() {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<G, FUSED>, NT, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<G, FUSED, FUSED>, NT, 0) != hipSuccess)
         return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     return per_cu * cus;
@@ -471,9 +496,9 @@ extern "C" int g3k_decode(const g3k_decode_args *a, int fused, void *stream) {
     if (a->n_splits < 1 || a->n_splits > G3K_MAX_SPLITS || a->rows_per_split % G3K_SPLIT_GRAIN)
         return (int)hipErrorInvalidValue;
     switch (a->group) {
-        case 1: return (int)(fused ? launch<1, true>(a, st) : launch<1, false>(a, st));
-        case 2: return (int)(fused ? launch<2, true>(a, st) : launch<2, false>(a, st));
-        case 4: return (int)(fused ? launch<4, true>(a, st) : launch<4, false>(a, st));
+        case 1: return (int)launch_g<1>(a, fused, st);
+        case 2: return (int)launch_g<2>(a, fused, st);
+        case 4: return (int)launch_g<4>(a, fused, st);
         default: return (int)hipErrorInvalidValue;
     }
 }

@@ -49,6 +49,7 @@ typedef struct {
     float *out;            /* [H_q][D] */
     float *ws_acc;         /* [H_kv][G3K_MAX_SPLITS][group][D] split partials */
     float *ws_ml;          /* [H_kv][G3K_MAX_SPLITS][group][2] (max, sum) */
+    int nt_loads;          /* fused decode: K/V rows through non-temporal buffer loads */
     void *ev0, *ev1;       /* hipEvent_t: begin / end of decode_kernel's dispatch, or NULL */
 } g3k_decode_args;
 
@@ -93,6 +94,13 @@ typedef struct {
 } g3k_rope_write_args;
 
 int g3k_rope_write(const g3k_rope_write_args *a, void *stream);
+
+/* Cache rows from the reference layout: rows [n][n_kv_heads][D] (device) ->
+ * dst + h*head_stride + (slot + i)*D for head h, row i, in one launch for
+ * every head (instead of a strided copy per head).  to_rows != 0 runs the
+ * other way (cache -> rows). */
+int g3k_kv_scatter(float *dst_k, float *dst_v, float *rows_k, float *rows_v, int n, int n_kv_heads,
+                   long long head_stride, int slot, int to_rows, void *stream);
 
 /* Prefill staging of key rows kk0..kk0+cnt-1 (key index kk = position -
  * kstart): K (already normed + rotated, fp32) -> fp16 hi | lo rows of

@@ -110,3 +110,40 @@ extern "C" int g3k_rope_write(const g3k_rope_write_args *a, void *stream) {
     hipLaunchKernelGGL(rope_write_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, *a);
     return (int)hipGetLastError();
 }
+
+namespace {
+
+// Rows in the reference layout [n][H_kv][D] <-> the head-major cache: one
+// thread per float4, consecutive threads along a row (coalesced on both
+// sides: a cache row is contiguous, and so is a reference-layout head row).
+__global__ __launch_bounds__(256) void kv_scatter_kernel(float *ck, float *cv, float *rk, float *rv, int n,
+                                                         int n_kv, long long head_stride, int slot,
+                                                         int to_rows) {
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long per_mat = (long long)n * n_kv * (D / 4);
+    if (t >= 2 * per_mat) return;
+    const int mat = (int)(t / per_mat);
+    const long long r = t % per_mat;
+    const int c4 = (int)(r % (D / 4));
+    const long long hr = r / (D / 4);
+    const int h = (int)(hr % n_kv), i = (int)(hr / n_kv);
+    float4 *rows = reinterpret_cast<float4 *>(mat ? rv : rk) + ((size_t)i * n_kv + h) * (D / 4) + c4;
+    float4 *cache = reinterpret_cast<float4 *>((mat ? cv : ck) + (size_t)h * head_stride + (size_t)(slot + i) * D) + c4;
+    if (to_rows)
+        *rows = *cache;
+    else
+        *cache = *rows;
+}
+
+}  // namespace
+
+extern "C" int g3k_kv_scatter(float *dst_k, float *dst_v, float *rows_k, float *rows_v, int n, int n_kv_heads,
+                              long long head_stride, int slot, int to_rows, void *stream) {
+    if (n <= 0) return 0;
+    const long long threads = 2LL * n * n_kv_heads * (D / 4);
+    const long long blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(kv_scatter_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dst_k, dst_v,
+                       rows_k, rows_v, n, n_kv_heads, head_stride, slot, to_rows);
+    return (int)hipGetLastError();
+}

@@ -145,6 +145,8 @@ struct g3attn_ctx {
     int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
     int n_cu;       /* compute units of the device */
+    /* decode: non-temporal cache loads (G3ATTN_DECODE_NT=0 turns them off) */
+    int nt_loads;
 };
 
 static void prof_destroy(g3attn_ctx *c) {
@@ -280,6 +282,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         c->prefill_qpw = (qpw && atoi(qpw) == 32) ? 32 : 16;
         const char *sch = getenv("G3ATTN_PREFILL_SCHED");
         c->prefill_sched = sch ? atoi(sch) : 1;
+        const char *nt = getenv("G3ATTN_DECODE_NT");
+        c->nt_loads = nt ? atoi(nt) != 0 : 1;
         if (c->min_rows < G3K_SPLIT_GRAIN) c->min_rows = G3K_SPLIT_GRAIN;
     }
 
@@ -494,6 +498,7 @@ int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, cons
     a.out = attn_out;
     a.ws_acc = c->ws_acc;
     a.ws_ml = c->ws_ml;
+    a.nt_loads = c->nt_loads;
     hipSetDevice(c->device);
     int rc = prof_slot(c, 0, &a.ev0, &a.ev1);
     if (rc) return rc;
@@ -605,6 +610,10 @@ int g3attn_kv_append(g3attn_ctx *c, int layer, int start_pos, int n, const float
     return G3_OK;
 }
 
+/* Host rows in the reference layout [n][H_kv][D] <-> cache slots
+ * slot..slot+n-1: one 1-D copy per matrix through the staging buffer, and
+ * one kernel between the staging and the head-major cache (instead of a
+ * strided 2-D copy per head and matrix). */
 static int kv_copy(g3attn_ctx *c, int layer, int slot, int n, float *k_rows, float *v_rows,
                    int to_device, const char *fn) {
     if (!check_layer(c, layer, fn)) return G3_ERR_INVALID_ARG;
@@ -616,22 +625,20 @@ static int kv_copy(g3attn_ctx *c, int layer, int slot, int n, float *k_rows, flo
     if (n == 0) return G3_OK;
     const int H = c->cfg.num_kv_heads;
     const size_t hs = (size_t)c->rows[layer] * D;
+    const size_t mb = (size_t)n * H * D * sizeof(float);
     hipSetDevice(c->device);
-    for (int h = 0; h < H; h++) {
-        float *dk = c->kc[layer] + h * hs + (size_t)slot * D;
-        float *dv = c->vc[layer] + h * hs + (size_t)slot * D;
-        const size_t row = D * sizeof(float), pitch = (size_t)H * row;
-        if (to_device) {
-            HIP_TRY(hipMemcpy2DAsync(dk, row, k_rows + (size_t)h * D, pitch, row, n,
-                                     hipMemcpyHostToDevice, c->stream), fn);
-            HIP_TRY(hipMemcpy2DAsync(dv, row, v_rows + (size_t)h * D, pitch, row, n,
-                                     hipMemcpyHostToDevice, c->stream), fn);
-        } else {
-            HIP_TRY(hipMemcpy2DAsync(k_rows + (size_t)h * D, pitch, dk, row, row, n,
-                                     hipMemcpyDeviceToHost, c->stream), fn);
-            HIP_TRY(hipMemcpy2DAsync(v_rows + (size_t)h * D, pitch, dv, row, row, n,
-                                     hipMemcpyDeviceToHost, c->stream), fn);
-        }
+    int rc = grow_big(c, 2 * mb);
+    if (rc) return rc;
+    float *sk = (float *)c->d_big, *sv = (float *)((unsigned char *)c->d_big + mb);
+    if (to_device) {
+        HIP_TRY(hipMemcpyAsync(sk, k_rows, mb, hipMemcpyHostToDevice, c->stream), fn);
+        HIP_TRY(hipMemcpyAsync(sv, v_rows, mb, hipMemcpyHostToDevice, c->stream), fn);
+    }
+    rc = g3k_kv_scatter(c->kc[layer], c->vc[layer], sk, sv, n, H, (long long)hs, slot, !to_device, c->stream);
+    if (rc) return hip_fail((hipError_t)rc, fn);
+    if (!to_device) {
+        HIP_TRY(hipMemcpyAsync(k_rows, sk, mb, hipMemcpyDeviceToHost, c->stream), fn);
+        HIP_TRY(hipMemcpyAsync(v_rows, sv, mb, hipMemcpyDeviceToHost, c->stream), fn);
     }
     HIP_TRY(hipStreamSynchronize(c->stream), fn);
     return G3_OK;
@@ -1820,7 +1827,6 @@ int g3attn_gqa_noalloc(float *output, const float *q, const float *k_cache, cons
     if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa_noalloc launch");
     return G3_OK;
 }
-
 
 /* Host-pointer GEMV through the same process-wide stream; its own grow-on-
  * demand device buffer holds A, x and y. */

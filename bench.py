@@ -763,9 +763,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("decode_kernel<2,true>@configs[1]"),
+            "traffic": measured_traffic("decode_kernel<2,true,true>@configs[1]"),
             "traffic_source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-            "kernel": "decode_kernel<2,true>",
+            "kernel": "decode_kernel<2,true,true>",
             "kernel_us": round(kernel_s * 1e6, 3),
             "call_us": round(call_s * 1e6, 3),
         },

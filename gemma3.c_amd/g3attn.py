@@ -71,7 +71,7 @@ def lib():
     L.g3attn_is_global_layer.argtypes = [C.c_int]
     L.g3attn_is_global_layer.restype = C.c_int
     L.g3attn_rope_precompute.argtypes = [_f32p, C.c_int, C.c_int, C.c_float]
-    L.g3attn_create.argtypes = [C.POINTER(Config), C.c_int, _f32p, _f32p]
+    L.g3attn_create.argtypes = [C.POINTER(Config), C.c_int, C.c_void_p, C.c_void_p]
     L.g3attn_create.restype = _vp
     L.g3attn_destroy.argtypes = [_vp]
     L.g3attn_reset.argtypes = [_vp]
@@ -104,6 +104,7 @@ def lib():
                                                 _vp, _vp, _vp]
     L.g3attn_forward_device.argtypes = [_vp, C.c_void_p, C.c_int, C.c_int, _vp, C.c_int, _vp]
     L.g3attn_upload_weights.argtypes = [_vp, C.c_void_p]
+    L.g3attn_upload_rope.argtypes = [_vp, _f32p, _f32p, C.c_int, C.c_int]
     L.g3attn_device_weights.argtypes = [_vp]
     L.g3attn_device_weights.restype = C.c_void_p
     L.g3attn_forward_token.argtypes = [_vp, C.c_int, C.c_int, C.c_void_p, C.c_int]
@@ -119,7 +120,7 @@ def lib():
                  "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
                  "g3attn_prefill_tokens", "g3attn_matmul_bf16_device",
                  "g3attn_prefill_forward_device", "g3attn_forward_token_device",
-                 "g3attn_gqa_noalloc"):
+                 "g3attn_gqa_noalloc", "g3attn_upload_rope"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -236,19 +237,34 @@ class Context:
     """A device context: the per-layer KV cache, RoPE tables and stream."""
 
     def __init__(self, cfg: Config | None = None, max_context: int | None = None,
-                 rope_local: np.ndarray | None = None, rope_global: np.ndarray | None = None):
+                 rope_local: np.ndarray | None = None, rope_global: np.ndarray | None = None,
+                 defer_rope: bool = False):
+        """Tables default to g3attn_rope_precompute's; defer_rope creates the
+        context without tables (NULL), for a later upload_rope."""
         self.cfg = cfg if cfg is not None else default_config()
         self.max_context = int(max_context if max_context is not None else self.cfg.max_context)
-        if rope_local is None:
-            rope_local = rope_precompute(self.max_context, self.cfg.rope_theta_local)
-        if rope_global is None:
-            rope_global = rope_precompute(self.max_context, self.cfg.rope_theta_global)
+        if defer_rope:
+            rope_local = rope_global = None
+        else:
+            if rope_local is None:
+                rope_local = rope_precompute(self.max_context, self.cfg.rope_theta_local)
+            if rope_global is None:
+                rope_global = rope_precompute(self.max_context, self.cfg.rope_theta_global)
+            rope_local = np.ascontiguousarray(rope_local, dtype=np.float32)
+            rope_global = np.ascontiguousarray(rope_global, dtype=np.float32)
         self.rope_local, self.rope_global = rope_local, rope_global
         self._h = lib().g3attn_create(C.byref(self.cfg), self.max_context,
-                                      np.ascontiguousarray(rope_local, dtype=np.float32),
-                                      np.ascontiguousarray(rope_global, dtype=np.float32))
+                                      None if rope_local is None else rope_local.ctypes.data,
+                                      None if rope_global is None else rope_global.ctypes.data)
         if not self._h:
             raise G3AttnError(ERR_INVALID_ARG, last_error())
+
+    def upload_rope(self, rope_local: np.ndarray, rope_global: np.ndarray, max_context: int | None = None,
+                    head_dim: int = 256):
+        """g3attn_upload_rope (gemma3_metal_upload_rope): replace both tables."""
+        n = self.max_context if max_context is None else int(max_context)
+        _check(lib().g3attn_upload_rope(self._h, np.ascontiguousarray(rope_local, dtype=np.float32),
+                                        np.ascontiguousarray(rope_global, dtype=np.float32), n, head_dim))
 
     @property
     def handle(self):

@@ -96,6 +96,7 @@ struct g3attn_ctx {
     int max_context, device, group;
     hipStream_t stream;
     float *rope_local, *rope_global;
+    int have_rope;     /* both tables uploaded (at create or by g3attn_upload_rope) */
     float **kc, **vc;
     int *rows;
     float *ws_acc, *ws_ml;
@@ -193,6 +194,22 @@ static void ctx_free(g3attn_ctx *c) {
     free(c);
 }
 
+/* Host-forced failures for testing the caller's fallback paths: G3ATTN_FAULT
+ * is a comma-separated list of sites ("create", "upload", "forward").  A
+ * listed site fails as its real counterpart would (create returns NULL,
+ * upload returns -4, a forward returns -1) before any GPU work is issued. */
+static int fault_at(const char *site) {
+    const char *f = getenv("G3ATTN_FAULT");
+    const size_t n = strlen(site);
+    while (f && *f) {
+        const char *e = strchr(f, ',');
+        const size_t len = e ? (size_t)(e - f) : strlen(f);
+        if (len == n && strncmp(f, site, n) == 0) return 1;
+        f = e ? e + 1 : NULL;
+    }
+    return 0;
+}
+
 static int alloc_dev(void **p, size_t bytes, const char *what) {
     hipError_t e = hipMalloc(p, bytes ? bytes : 1);
     if (e != hipSuccess) {
@@ -210,8 +227,12 @@ static size_t ws_slots(int n_kv) { return (size_t)n_kv * G3K_MAX_SPLITS; }
 g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
                           const float *rope_local, const float *rope_global) {
     g_err[0] = 0;
-    if (!cfg || !rope_local || !rope_global || max_context <= 0) {
-        set_err("g3attn_create: null argument or max_context <= 0");
+    if (!cfg || !rope_local != !rope_global || max_context <= 0) {
+        set_err("g3attn_create: null config, one RoPE table without the other, or max_context <= 0");
+        return NULL;
+    }
+    if (fault_at("create")) {
+        set_err("g3attn_create: injected failure (G3ATTN_FAULT=create)");
         return NULL;
     }
     if (!check_shape(cfg->num_heads, cfg->num_kv_heads, cfg->head_dim)) return NULL;
@@ -245,9 +266,12 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
     const size_t rope_bytes = (size_t)max_context * D * sizeof(float);
     if (!alloc_dev((void **)&c->rope_local, rope_bytes, "rope table")) goto fail;
     if (!alloc_dev((void **)&c->rope_global, rope_bytes, "rope table")) goto fail;
-    if (hipMemcpy(c->rope_local, rope_local, rope_bytes, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(c->rope_global, rope_global, rope_bytes, hipMemcpyHostToDevice) != hipSuccess)
-        goto fail_rt;
+    if (rope_local) {
+        if (hipMemcpy(c->rope_local, rope_local, rope_bytes, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(c->rope_global, rope_global, rope_bytes, hipMemcpyHostToDevice) != hipSuccess)
+            goto fail_rt;
+        c->have_rope = 1;
+    }
 
     const int L = cfg->num_layers;
     c->kc = (float **)calloc((size_t)L, sizeof(float *));
@@ -456,10 +480,38 @@ static int check_layer(const g3attn_ctx *c, int layer, const char *fn) {
     return 1;
 }
 
+static int check_rope(const g3attn_ctx *c, const char *fn) {
+    if (!c->have_rope) {
+        set_err("%s: RoPE tables not uploaded (g3attn_create without tables needs g3attn_upload_rope)", fn);
+        return 0;
+    }
+    return 1;
+}
+
+int g3attn_upload_rope(g3attn_ctx *c, const float *rope_local, const float *rope_global, int max_context,
+                       int head_dim) {
+    if (!c || !rope_local || !rope_global) {
+        set_err("g3attn_upload_rope: null context or table");
+        return G3_ERR_INVALID_ARG;
+    }
+    if (max_context != c->max_context || head_dim != D) {
+        set_err("g3attn_upload_rope: tables of %d positions x head_dim %d; the context needs %d x %d",
+                max_context, head_dim, c->max_context, D);
+        return G3_ERR_INVALID_ARG;
+    }
+    hipSetDevice(c->device);
+    const size_t bytes = (size_t)max_context * D * sizeof(float);
+    HIP_TRY(hipStreamSynchronize(c->stream), "g3attn_upload_rope");
+    HIP_TRY(hipMemcpy(c->rope_local, rope_local, bytes, hipMemcpyHostToDevice), "g3attn_upload_rope");
+    HIP_TRY(hipMemcpy(c->rope_global, rope_global, bytes, hipMemcpyHostToDevice), "g3attn_upload_rope");
+    c->have_rope = 1;
+    return G3_OK;
+}
+
 int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
                          const float *v, const uint16_t *q_norm, const uint16_t *k_norm,
                          float *attn_out) {
-    if (!check_layer(c, layer, "g3attn_decode")) return G3_ERR_INVALID_ARG;
+    if (!check_layer(c, layer, "g3attn_decode") || !check_rope(c, "g3attn_decode")) return G3_ERR_INVALID_ARG;
     if (!q || !k || !v || !attn_out || pos < 0) {
         set_err("g3attn_decode: null buffer or pos < 0");
         return G3_ERR_INVALID_ARG;
@@ -545,7 +597,7 @@ int g3attn_decode(g3attn_ctx *c, int layer, int pos, const float *q, const float
 
 int g3attn_kv_append_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *K,
                             const float *V, const uint16_t *k_norm) {
-    if (!check_layer(c, layer, "g3attn_kv_append")) return G3_ERR_INVALID_ARG;
+    if (!check_layer(c, layer, "g3attn_kv_append") || !check_rope(c, "g3attn_kv_append")) return G3_ERR_INVALID_ARG;
     if (n < 0 || start_pos < 0 || (n > 0 && (!K || !V))) {
         set_err("g3attn_kv_append: bad arguments");
         return G3_ERR_INVALID_ARG;
@@ -587,7 +639,7 @@ int g3attn_kv_append_device(g3attn_ctx *c, int layer, int start_pos, int n, cons
 
 int g3attn_kv_append(g3attn_ctx *c, int layer, int start_pos, int n, const float *K,
                      const float *V, const uint16_t *k_norm) {
-    if (!check_layer(c, layer, "g3attn_kv_append")) return G3_ERR_INVALID_ARG;
+    if (!check_layer(c, layer, "g3attn_kv_append") || !check_rope(c, "g3attn_kv_append")) return G3_ERR_INVALID_ARG;
     if (n <= 0) return n == 0 ? G3_OK : G3_ERR_INVALID_ARG;
     if (!K || !V) {
         set_err("g3attn_kv_append: null buffer");
@@ -716,7 +768,7 @@ static int prefill_splits(int n, int hist, int nk, int window, int pb, int n_kv,
 int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
                           const float *K, const float *V, const uint16_t *q_norm,
                           const uint16_t *k_norm, float *attn_out) {
-    if (!check_layer(c, layer, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
+    if (!check_layer(c, layer, "g3attn_prefill") || !check_rope(c, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
     if (n < 0 || start_pos < 0 || (n > 0 && (!Q || !K || !V || !attn_out))) {
         set_err("g3attn_prefill: null buffer or negative start_pos / n");
         return G3_ERR_INVALID_ARG;
@@ -869,7 +921,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
 int g3attn_prefill(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
                    const float *K, const float *V, const uint16_t *q_norm,
                    const uint16_t *k_norm, float *attn_out) {
-    if (!check_layer(c, layer, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
+    if (!check_layer(c, layer, "g3attn_prefill") || !check_rope(c, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
     if (n < 0 || (n > 0 && (!Q || !K || !V || !attn_out))) {
         set_err("g3attn_prefill: null buffer or n < 0");
         return G3_ERR_INVALID_ARG;
@@ -1518,6 +1570,10 @@ int g3attn_upload_weights(g3attn_ctx *c, const void *weights) {
         set_err("g3attn_upload_weights: embed_tokens or norm is NULL");
         return G3_ERR_INVALID_ARG;
     }
+    if (fault_at("upload")) {
+        set_err("g3attn_upload_weights: injected device allocation failure (G3ATTN_FAULT=upload)");
+        return G3_ERR_OUT_OF_MEMORY;
+    }
     size_t n[13];
     layer_tensor_sizes(cfg, n);
     const size_t embed_n = (size_t)cfg->vocab_size * cfg->hidden_size, norm_n = (size_t)cfg->hidden_size;
@@ -1606,6 +1662,10 @@ static int forward_uploaded_logits(g3attn_ctx *c, const char *who) {
  * vs 2.39 ms per token.  The host issues the launches well ahead of the
  * GPU, so nothing waits on their submission.) */
 static int forward_uploaded(g3attn_ctx *c, int token_id, int pos, int want_logits, const char *who) {
+    if (fault_at("forward")) {
+        set_err("%s: injected GPU failure (G3ATTN_FAULT=forward)", who);
+        return G3_ERR_INVALID_ARG;
+    }
     if (!c->have_wt) {
         set_err("%s: no weights uploaded (g3attn_upload_weights)", who);
         return G3_ERR_INVALID_ARG;
@@ -1669,6 +1729,10 @@ int g3attn_prefill_tokens(g3attn_ctx *c, const int *tokens, int num_tokens, int 
                     c->cfg.vocab_size);
             return G3_ERR_INVALID_ARG;
         }
+    if (fault_at("forward")) {
+        set_err("g3attn_prefill_tokens: injected GPU failure (G3ATTN_FAULT=forward)");
+        return G3_ERR_INVALID_ARG;
+    }
     if (!c->have_wt) {
         set_err("g3attn_prefill_tokens: no weights uploaded (g3attn_upload_weights)");
         return G3_ERR_INVALID_ARG;

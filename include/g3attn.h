@@ -74,9 +74,25 @@ void g3attn_rope_precompute(float *freqs, int max_pos, int head_dim, float theta
  * ([max_context][head_dim/2][2], from gemma3_transformer.c:870-883; the Metal
  * backend uploads them the same way, gemma3_metal.m:603-614).  Replaces
  * gemma3_metal_init + gemma3_metal_upload_rope (gemma3_metal.h:26, 37-39).
- * Returns NULL on failure (message in g3attn_last_error). */
+ * Both tables may be NULL, as gemma3_metal_init takes none: they are then
+ * uploaded with g3attn_upload_rope, and the attention calls return -1 until
+ * they are.  Returns NULL on failure (message in g3attn_last_error).
+ *
+ * Failure injection, for testing a caller's fallback: the environment
+ * variable G3ATTN_FAULT, a comma-separated list read at each call, makes the
+ * listed sites fail before any GPU work: "create" (g3attn_create returns
+ * NULL), "upload" (g3attn_upload_weights returns -4, as a failed device
+ * allocation does) and "forward" (g3attn_forward_token[_device] and
+ * g3attn_prefill_tokens return -1, as a GPU runtime error does). */
 g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
                           const float *rope_local, const float *rope_global);
+
+/* gemma3_metal_upload_rope (gemma3_metal.h:37-39, called at
+ * gemma3_transformer.c:893-895): copies the engine's local and global RoPE
+ * tables [max_context][head_dim/2][2] to the device, replacing the context's.
+ * max_context must equal the context's and head_dim must be 256, else -1. */
+int g3attn_upload_rope(g3attn_ctx *ctx, const float *rope_local, const float *rope_global,
+                       int max_context, int head_dim);
 
 /* gemma3_kv_cache_free (gemma3_transformer.c:216-223) + gemma3_metal_free. */
 void g3attn_destroy(g3attn_ctx *ctx);

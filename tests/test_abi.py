@@ -103,6 +103,54 @@ def test_invalid_shapes_rejected_before_device_use():
     for bad in (dict(head_dim=128), dict(num_heads=6), dict(num_heads=8, num_kv_heads=1),
                 dict(num_layers=0), dict(sliding_window=0)):
         cfg = G.default_config(max_context=16, **bad)
-        h = G.lib().g3attn_create(C.byref(cfg), 16, t, t)
+        h = G.lib().g3attn_create(C.byref(cfg), 16, t.ctypes.data, t.ctypes.data)
         assert not h
         assert G.last_error()
+
+
+def test_create_needs_both_tables_or_neither():
+    t = O.rope_table(16, 1e4)
+    cfg = G.default_config(max_context=16)
+    assert not G.lib().g3attn_create(C.byref(cfg), 16, t.ctypes.data, None)
+    assert "RoPE table" in G.last_error()
+    assert not G.lib().g3attn_create(C.byref(cfg), 16, None, t.ctypes.data)
+
+
+def test_injected_create_failure(monkeypatch):
+    """G3ATTN_FAULT=create fails g3attn_create before any device use, with
+    its cause in the message; the list is comma-separated, sites match whole."""
+    t = O.rope_table(16, 1e4)
+    cfg = G.default_config(max_context=16)
+    for val in ("create", "upload,create", "create,forward"):
+        monkeypatch.setenv("G3ATTN_FAULT", val)
+        assert not G.lib().g3attn_create(C.byref(cfg), 16, t.ctypes.data, t.ctypes.data)
+        assert "injected" in G.last_error(), val
+    if not _gpu_present():
+        monkeypatch.setenv("G3ATTN_FAULT", "creat,createx,upload")
+        assert not G.lib().g3attn_create(C.byref(cfg), 16, t.ctypes.data, t.ctypes.data)
+        assert "injected" not in G.last_error() and "device" in G.last_error()
+
+
+def test_upload_rope_rejects_a_null_context():
+    t = O.rope_table(16, 1e4)
+    assert G.lib().g3attn_upload_rope(None, t, t, 16, 256) == G.ERR_INVALID_ARG
+    assert "null" in G.last_error()
+
+
+@pytest.mark.skipif(not os.path.exists("/root/reference/gemma3_transformer.c"),
+                    reason="reference sources not present on this machine")
+def test_backend_hook_declares_the_engines_functions():
+    """include/g3backend.h declares exactly the backend functions that
+    gemma3_transformer.c declares under USE_MPS (:17-31), and
+    libg3backend.so exports them."""
+    import re
+    src = open("/root/reference/gemma3_transformer.c").read()
+    block = src[src.index("#ifdef USE_MPS"):]
+    block = block[:block.index("#endif")]
+    want = set(re.findall(r"\b(gemma3_metal_\w+)\s*\(", block))
+    hdr = re.sub(r"/\*.*?\*/", "", open(os.path.join(REPO, "include", "g3backend.h")).read(), flags=re.S)
+    have = set(re.findall(r"\b(gemma3_metal_\w+)\s*\(", hdr))
+    assert len(want) == 7 and want <= have and have - want == {"gemma3_metal_available"}
+    lib = C.CDLL(os.path.join(REPO, "gemma3.c_amd", "lib", "libg3backend.so"))
+    for name in have:
+        assert hasattr(lib, name), name

@@ -121,6 +121,27 @@ def test_decode_gqa_groups(n_heads, n_kv):
         ctx.close()
 
 
+def test_tables_uploaded_after_create():
+    """A context created without RoPE tables (the backend hook's init, which
+    takes none) refuses attention calls until g3attn_upload_rope, then matches
+    the oracle on both layer kinds; tables of the wrong size are refused."""
+    cfg = G.default_config(max_context=2048, num_layers=6)
+    ctx = G.Context(cfg, 2048, defer_rope=True)
+    try:
+        q = np.zeros(QS, np.float32)
+        k = np.zeros(KS, np.float32)
+        assert ctx.decode_rc(0, 5, q, k, k) == G.ERR_INVALID_ARG
+        assert "RoPE" in G.last_error()
+        tl, tg = O.rope_table(2048, 10000.0), O.rope_table(2048, 1e6)
+        with pytest.raises(G.G3AttnError):
+            ctx.upload_rope(tl[:1024], tg[:1024], max_context=1024)
+        ctx.upload_rope(tl, tg)
+        for layer, pos in ((0, 700), (5, 1500)):
+            _check(DecodeCase(13, layer=layer, pos=pos, max_context=2048), ctx, "rope-upload")
+    finally:
+        ctx.close()
+
+
 def test_no_norm(ctx8k):
     """q_norm = k_norm = NULL skips the QK-norm (gemma3_transformer.c:295)."""
     _check(DecodeCase(9, layer=5, pos=300, max_context=8192, norm=False), ctx8k, "no-norm")

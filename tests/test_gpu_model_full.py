@@ -1,0 +1,103 @@
+"""The whole-model rows at Gemma3-4B shapes (34 layers, hidden 2560,
+intermediate 10240, vocab 262208, 8 / 4 heads of 256, window 1024), with
+random bf16 weights: the shapes the bench measures, checked for values.
+
+- Token forward (g3attn_upload_weights + g3attn_forward_token, replacing
+  gemma3_transformer_forward, gemma3_transformer.c:396-512) for three tokens
+  against the oracle's restatement of the same forward (g3o_forward_seq) on
+  the same host weights.  fp32 throughout on both sides; the bar is 1e-4 x
+  RMS per logits row, as for the small-model golden.
+- Batched prefill (g3attn_prefill_tokens for 2048 tokens: MFMA GEMM
+  projections + the prefill attention kernel, replacing
+  gemma3_transformer_prefill_batched, :526-787) against the token forward
+  looped over the same 2048 tokens (the engine's non-BLAS prefill,
+  :814-821), then one decode step after each.  The GEMMs take x as bf16 hi +
+  lo (16 significant bits) where the GEMV reads fp32 x; the bar is 1e-3 x
+  RMS of the last logits row, with the measured figure printed.
+
+Weights: N(0,1) x 2^-6 (norm gains N(0,1) x 2^-3) from torch's generator on
+the GPU, rounded to bf16 and copied to the host, so both sides read the same
+bits.  About 7.8 GB of host and device memory.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import O, g3attn, rel_err
+
+pytestmark = pytest.mark.gpu
+
+G = g3attn()
+H, I, V, L = 2560, 10240, 262208, 34
+QS, KS = 8 * 256, 4 * 256
+MAXCTX = 4096
+
+
+@pytest.fixture(scope="module")
+def model():
+    import torch
+    torch.cuda.set_device(0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x6A33)
+
+    def w(n, shift=6):
+        t = torch.randn(n, device="cuda", generator=gen, dtype=torch.float32) * (2.0 ** -shift)
+        return t.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+
+    embed = w(V * H)
+    layers = []
+    for _ in range(L):
+        layers.append(dict(input_layernorm=w(H, 3), q_proj=w(QS * H), k_proj=w(KS * H), v_proj=w(KS * H),
+                           o_proj=w(H * QS), q_norm=w(256, 3), k_norm=w(256, 3),
+                           post_attention_layernorm=w(H, 3), gate_proj=w(I * H), up_proj=w(I * H),
+                           down_proj=w(H * I), pre_feedforward_layernorm=w(H, 3),
+                           post_feedforward_layernorm=w(H, 3)))
+    norm = w(H, 3)
+    torch.cuda.synchronize()
+    print("[full model] weights generated", flush=True)
+    cfg = G.default_config(max_context=MAXCTX)
+    assert (cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers) == (H, I, V, L)
+    ctx = G.Context(cfg, MAXCTX)
+    HW, keep = G.host_weights(embed, layers, norm)
+    ctx.upload_weights(HW)
+    del keep
+    print("[full model] uploaded", flush=True)
+    yield ctx, embed, layers, norm
+    ctx.close()
+
+
+def test_forward_full_shapes_vs_oracle(model):
+    ctx, embed, layers, norm = model
+    tokens = np.array([5, 70001, 262207], np.int32)
+    ctx.reset()
+    got = np.stack([ctx.forward_token(int(t), i) for i, t in enumerate(tokens)])
+    print("[full model] gpu forward done; oracle forward (one core)", flush=True)
+    want, _ = O.forward_seq(O.Config(num_layers=L, max_context=64), H, I, tokens, embed, layers, norm)
+    for i in range(len(tokens)):
+        err = rel_err(got[i], want[i])
+        print(f"[full forward] token {i} (pos {i}): logits rel_err={err:.3e}", flush=True)
+        assert err < 1e-4, (i, err)
+    assert np.array_equal(got.argmax(axis=1), want.argmax(axis=1))
+
+
+def test_batched_prefill_2048_vs_token_loop(model):
+    ctx, _, _, _ = model
+    n = 2048
+    tokens = (np.arange(n + 1, dtype=np.int64) * 7919 % (V - 2) + 2).astype(np.int32)
+    ctx.reset()
+    loop = None
+    for i in range(n):
+        last = ctx.forward_token(int(tokens[i]), i, compute_logits=(i == n - 1))
+        if i == n - 1:
+            loop = last
+    loop_next = ctx.forward_token(int(tokens[n]), n)
+    ctx.reset()
+    batched = ctx.prefill_tokens(tokens[:n])
+    batched_next = ctx.forward_token(int(tokens[n]), n)
+    e1, e2 = rel_err(batched, loop), rel_err(batched_next, loop_next)
+    print(f"[full prefill] N={n}: last logits rel_err={e1:.3e}; next decode rel_err={e2:.3e}", flush=True)
+    assert e1 < 1e-3 and e2 < 1e-3
+    assert int(np.argmax(batched)) == int(np.argmax(loop))
+    assert int(np.argmax(batched_next)) == int(np.argmax(loop_next))

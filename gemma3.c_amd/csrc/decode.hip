@@ -260,6 +260,13 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     float kk[R][4][4], vv[R][4][4];
     int base = c0 + wave * ROWS_PER_WAVE_STEP;
     if (base < c1) load_step<R, NTL>(kk, vv, kbase, vbase, p.row_stride, p.head_stride, base, c1, p.skip, grp, c);
+    // the new token's k / v (split 0, wave 0) are in flight during the prologue too
+    const bool seeds = FUSED && split == 0 && wave == 0;
+    float kn[4][4], vn[4][4];
+    if (seeds) {
+        load16(kn, p.k_new + (size_t)kvh * D, c);
+        load16(vn, p.v_new + (size_t)kvh * D, c);
+    }
 
     // ---- query: this lane's 16 dims of each of the G query heads ----
     float qv[G][4][4];
@@ -295,10 +302,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     }
 
     // ---- the new token (fused decode): split 0, wave 0 seeds its state with it ----
-    if (FUSED && split == 0 && wave == 0) {
-        float kn[4][4], vn[4][4];
-        load16(kn, p.k_new + (size_t)kvh * D, c);
-        load16(vn, p.v_new + (size_t)kvh * D, c);
+    if (seeds) {
         norm_rope16(kn, p.q_norm ? p.k_norm : nullptr, p.eps, cs, sn, c);
         if (grp == 0) {
             store16(p.kc + (size_t)kvh * p.head_stride + (size_t)p.new_slot * p.row_stride, kn, c);

@@ -74,10 +74,12 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// A is read with plain loads: non-temporal ones stream faster, but the
-// decode kernel's measurements showed them returning stale values for memory
-// that a host -> device copy rewrote after kernels had touched it, and A may
-// be re-uploaded in place (g3attn_upload_weights, a caller's own buffers).
+// A streams through a buffer descriptor per matrix with the non-temporal
+// cache policy (read once per call, not worth keeping in L2); the byte
+// offset of a row chunk fits 32 bits (the launcher checks the matrix size).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mat_rsrc(const uint16_t *base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // NA dot products: RPW consecutive rows of one matrix, or (GEGLU) the same
 // rows of the gate and up matrices.  Without KS each wave owns its own RPW
@@ -97,11 +99,13 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
     const float *x = a.x;
     const int r0 = KS ? row0 : row0 + wave * RPW;
     const uint16_t *rows[NA];
+    unsigned roff[NA];   // byte offset of each row in its matrix
 #pragma unroll
     for (int j = 0; j < NA; j++) {
         const int jr = GEGLU ? j % RPW : j;
         const int row = r0 + jr < M ? r0 + jr : M - 1;
         rows[j] = a.A[GEGLU ? j / RPW : m] + (size_t)row * K;
+        roff[j] = (unsigned)row * (unsigned)K * 2u;
     }
     float acc[NA];
 #pragma unroll
@@ -112,6 +116,10 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
         const int q = KS ? (nch + NW - 1) / NW : nch;
         const int cbeg = KS ? wave * q : 0, cend = KS ? min(cbeg + q, nch) : nch;
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        __amdgpu_buffer_rsrc_t rs[GEGLU ? 2 : 1];
+#pragma unroll
+        for (int t = 0; t < (GEGLU ? 2 : 1); t++)
+            rs[t] = mat_rsrc(a.A[GEGLU ? t : m], (unsigned)((size_t)M * K * 2));
         for (int base = cbeg; base < cend; base += 64 * CH) {
             uint4 w[NA][CH];
             float4 xa[CH], xb[CH];
@@ -120,8 +128,11 @@ __global__ __launch_bounds__(NT) void matvec_kernel(g3k_matvec_args a) {
                 const int c = base + lane + 64 * u;
                 const bool ok = c < cend;
 #pragma unroll
-                for (int j = 0; j < NA; j++)
-                    w[j][u] = ok ? *reinterpret_cast<const uint4 *>(rows[j] + 8 * c) : make_uint4(0, 0, 0, 0);
+                for (int j = 0; j < NA; j++) {
+                    const uint4 t = __builtin_bit_cast(
+                        uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[GEGLU ? j / RPW : 0], roff[j] + 16u * (ok ? c : 0), 0, 2));
+                    w[j][u] = ok ? t : make_uint4(0, 0, 0, 0);
+                }
                 xa[u] = ok ? x4[2 * c] : make_float4(0.f, 0.f, 0.f, 0.f);
                 xb[u] = ok ? x4[2 * c + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
@@ -189,6 +200,8 @@ extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
         rows += a->M[m];
     }
     if (rows > (1LL << 30)) return (int)hipErrorInvalidValue;
+    // the vector path addresses each matrix through a 32-bit byte offset
+    for (int m = 0; m < a->n_mat; m++) vec = vec && (long long)a->M[m] * a->K * 2 < (1LL << 32);
     hipStream_t st = (hipStream_t)stream;
     if (a->mode == G3K_MV_GEGLU) {
         if (a->n_mat != 2 || a->M[0] != a->M[1]) return (int)hipErrorInvalidValue;

@@ -36,10 +36,10 @@
 // deep, filled by gfx950's direct buffer -> LDS loads (buffer_load_dwordx4
 // ... lds: no staging registers; one wave instruction moves 1 KiB in lane
 // order; the addresses are a scalar buffer descriptor + one per-lane offset):
-//   K: one LDS row per key, fp16 hi (512 B) | lo (512 B), rows padded to
-//      1040 B and placed at slot kslot(key), so the 16 rows one fragment read
-//      touches hit 16 bank groups, and every fragment address is a per-lane
-//      base + an immediate offset;
+//   K: one 1 KiB LDS row per key, fp16 hi (512 B) | lo (512 B), its 16-byte
+//      chunks XOR-swizzled by key bits (kswz), so the 16 rows one fragment
+//      read touches hit 16 bank groups; every fragment address is one of
+//      four per-lane bases + an immediate offset;
 //   V^T: [256][32] bf16 (then the lo part), the four 16-byte chunks of a row
 //      XOR-swizzled by row bits 2-3 (conflict-free fragment reads).
 // Iteration kt computes the scores of tile kt + 1 and the P.V of tile kt,
@@ -60,11 +60,11 @@ using namespace g3k;
 constexpr int D = G3K_HEAD_DIM;
 constexpr int NT = 256;                      // staging kernel
 constexpr int BK = 32;                       // keys per tile
-constexpr int KROWB = 1040;                  // bytes per K row in LDS: hi | lo | pad
-constexpr int KTILEB = BK * KROWB;           // bytes of a K tile (33280)
+constexpr int KROWB = 1024;                  // bytes per K row in LDS: hi | lo
+constexpr int KTILEB = BK * KROWB;           // bytes of a K tile (32768)
 constexpr int VTILEB = D * BK * 2;           // bytes of a V^T tile, one part (16 KiB)
 constexpr int LDS_V0 = 2 * KTILEB;           // V ring after the K ring
-constexpr int LDS_BYTES = LDS_V0 + 2 * 2 * VTILEB;   // 132096
+constexpr int LDS_BYTES = LDS_V0 + 2 * 2 * VTILEB;   // 131072
 constexpr float NEG_BIG = -1.0e30f;
 constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 #ifndef G3K_KPF
@@ -165,12 +165,14 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 // d+12 (one bank residue) take the four chunk positions.
 __device__ __forceinline__ int vswz(int d) { return (d >> 2) & 3; }
 
-// LDS slot of key row r of a tile.  A K fragment read touches the rows
-// {0-3, 8-11, 16-19, 24-27} (or that set + 4) at one chunk; with 1040-byte
-// rows the bank group is slot % 16, so rows r and r + 16 would collide.
-// Flipping bit 2 of the upper half's rows makes each read set hit all 16
-// bank groups.
-__device__ __forceinline__ int kslot(int r) { return r ^ ((r >> 4) << 2); }
+// Chunk swizzle of key row r of a tile: logical 16-byte chunk c of the row
+// sits at chunk c ^ kswz(r).  A K fragment read touches the rows {0-3, 8-11,
+// 16-19, 24-27} (or that set + 4) at one logical chunk; with 1 KiB rows the
+// bank group of a chunk is its index % 16, and kswz maps each read set onto
+// all 16 values.  It replaced 1040-byte padded rows: the kernel's LDS
+// bank-conflict cycles fell from 4.0 to 1.33 per LDS instruction and
+// configs[3] from 588.6 to 578.6 us on one box.
+__device__ __forceinline__ int kswz(int r) { return ((r >> 3) << 2) | (r & 3); }
 
 // Raw buffer descriptor over [base, base + bytes): stride 0, the gfx9
 // family's dword-3 format word for untyped access.
@@ -178,15 +180,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, un
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// K tile kt -> LDS ring slot `dst`: 32 rows of 1 KiB (hi | lo), lane l moves
-// bytes 16 l .. 16 l + 15 of the row; 32 / NW rows per wave.
+// K tile kt -> LDS ring slot `dst`: 32 rows of 1 KiB (hi | lo); lane l moves
+// the row's logical chunk l ^ kswz(row) to LDS chunk l; 32 / NW rows per
+// wave.
 template <int NW>
 __device__ __forceinline__ void fetch_k(unsigned char *dst, __amdgpu_buffer_rsrc_t kr, int kt, int wave,
                                         int lane) {
 #pragma unroll
     for (int u = 0; u < 32 / NW; u++) {
         const int j = wave * (32 / NW) + u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(dst + kslot(j) * KROWB), 16, lane * 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(dst + j * KROWB), 16, (lane ^ kswz(j)) * 16,
                                                  (kt * BK + j) * (4 * D), 0, 0);
     }
 }
@@ -219,18 +222,18 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // k_hi q_lo, k_lo q_hi).  Every K fragment read from LDS feeds all NQB query
 // blocks; the fragments of d-step t + 1 are read while step t's MFMAs run.
 template <int NQB>
-__device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned char *st, int koff0,
-                                            int koff1, const half8 (&qh)[NQB][8],
+__device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned char *st, const int (&ka)[4],
+                                            const int (&kb)[4], const half8 (&qh)[NQB][8],
                                             const half8 (&ql)[NQB][8]) {
     constexpr int PF = G3K_KPF;       // d-steps of K fragments in flight
 #pragma unroll
     for (int b = 0; b < NQB; b++) s[b][0] = s[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     half8 f[PF + 1][4];
     auto load = [&](half8 (&r)[4], int t) {
-        r[0] = *reinterpret_cast<const half8 *>(st + koff0 + 64 * t);
-        r[1] = *reinterpret_cast<const half8 *>(st + koff0 + 512 + 64 * t);
-        r[2] = *reinterpret_cast<const half8 *>(st + koff1 + 64 * t);
-        r[3] = *reinterpret_cast<const half8 *>(st + koff1 + 512 + 64 * t);
+        r[0] = *reinterpret_cast<const half8 *>(st + ka[t & 3] + 256 * (t >> 2));
+        r[1] = *reinterpret_cast<const half8 *>(st + ka[t & 3] + 512 + 256 * (t >> 2));
+        r[2] = *reinterpret_cast<const half8 *>(st + kb[t & 3] + 256 * (t >> 2));
+        r[3] = *reinterpret_cast<const half8 *>(st + kb[t & 3] + 512 + 256 * (t >> 2));
     };
 #pragma unroll
     for (int t = 0; t < PF; t++) load(f[t], t);
@@ -394,8 +397,18 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // key 8 (m / 4) + 4 j + m % 4) at chunk g, and the V^T row ln of each
     // 16-dim block at its swizzled chunk g
     const int krow = 8 * (ln >> 2) + (ln & 3);
-    const int koff0 = kslot(krow) * KROWB + 16 * g;
-    const int koff1 = kslot(krow + 4) * KROWB + 16 * g;
+    // logical chunk g + 4 t of row r sits at chunk (g ^ fl) + 4 (t ^ fh), with
+    // fl = kswz(r) & 3 and fh = kswz(r) >> 2: four bases per row for t % 4,
+    // t / 4 as an immediate (kswz(krow + 4) == kswz(krow))
+    int koff0[4], koff1[4];
+    {
+        const int f = kswz(krow), fl = f & 3, fh = f >> 2;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            koff0[u] = krow * KROWB + 16 * (g ^ fl) + 64 * (u ^ fh);
+            koff1[u] = (krow + 4) * KROWB + 16 * (g ^ fl) + 64 * (u ^ fh);
+        }
+    }
     const int voff = ln * 64 + 16 * (g ^ vswz(ln));
 
     wait_fetch_all();

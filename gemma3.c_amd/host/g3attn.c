@@ -562,7 +562,9 @@ int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, cons
     a.out = attn_out;
     a.ws_acc = c->ws_acc;
     a.ws_ml = c->ws_ml;
-    a.nt_loads = c->nt_loads;
+    /* the non-temporal loads address a KV head's rows with 32-bit byte
+     * offsets: heads of 4 GiB or more (max_context >= 4M) take plain loads */
+    a.nt_loads = c->nt_loads && (size_t)c->rows[layer] * D * sizeof(float) < ((size_t)1 << 32);
     hipSetDevice(c->device);
     int rc = prof_slot(c, 0, &a.ev0, &a.ev1);
     if (rc) return rc;

@@ -41,11 +41,10 @@ constexpr int NT = 256;               // threads per workgroup
 constexpr int NW = NT / 64;           // waves per workgroup
 // Rows per lane-group per step (a wave step covers 4*R rows); G = 4 keeps
 // one row so its larger q / acc arrays fit without spills.  Only the R
-// values below are built and tested.  An R = 4 variant (one 64-row step per
-// workgroup at 8K, with the query moved to LDS to fit 256 VGPRs) returned
-// wrong outputs from its -O3 builds and correct ones, 40% slower, from -O1;
-// the cause was not found (undefined behaviour or a missing wait in that
-// variant's query-in-LDS code is as likely as a compiler fault).
+// values below are built and tested.  Builds of this kernel with R = 3 or
+// R = 4 (one wave per SIMD for R = 4) return wrong outputs at -O3, with plain
+// or non-temporal loads and with shuffle or permlane reductions; R = 1 and
+// R = 2 at the same launch bounds are correct.  The cause was not found.
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step

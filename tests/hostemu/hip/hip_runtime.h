@@ -1,0 +1,348 @@
+// hip/hip_runtime.h for the host-emulation build of the decode kernels.
+//
+// TEST INFRASTRUCTURE.  tests/hostemu/Makefile compiles
+// gemma3.c_amd/csrc/decode.hip as plain C++ (g++, -fsanitize=address,undefined)
+// with this directory first on the include path, so the kernels' own source
+// runs on the CPU under the sanitizers.  This header supplies the subset of
+// the HIP device language those kernels use, emulated on the host:
+//
+//   - A launch runs every workgroup of the grid in turn on one team of
+//     blockDim fibers (one ucontext per GPU thread, all on the calling OS
+//     thread), so 64 consecutive fibers form one wave64.  __shared__ becomes
+//     a function-local static: one copy, used by one workgroup at a time.
+//   - __syncthreads is a barrier over the team; every cross-lane operation
+//     (DPP, v_permlane16/32_swap, __shfl_xor) is an exchange through a
+//     per-wave buffer between two barriers over the wave's 64 fibers.  A
+//     barrier or cross-lane operation that not every lane reaches leaves no
+//     fiber runnable, and the launch aborts (on the GPU it would be
+//     undefined).
+//   - Buffer loads check their offset against the descriptor's num_records
+//     and abort on an out-of-range load instead of returning zero: the
+//     kernels clamp every row index, so none may go out of range.
+//   - DPP controls other than the ones the kernels use abort.
+//
+// Cross-lane semantics follow AMD's CDNA4 ISA descriptions of
+// DPP quad_perm / row_mirror / row_half_mirror, V_PERMLANE16_SWAP_B32 and
+// V_PERMLANE32_SWAP_B32, and ds_bpermute-based __shfl_xor.
+#ifndef G3_HOSTEMU_HIP_RUNTIME_H
+#define G3_HOSTEMU_HIP_RUNTIME_H
+
+#include <array>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <math.h>
+#include <functional>
+#include <ucontext.h>
+#include <vector>
+#if defined(__SANITIZE_ADDRESS__)
+#include <sanitizer/common_interface_defs.h>
+#endif
+
+// ---- language keywords ------------------------------------------------------
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __shared__ static
+#define __launch_bounds__(...)
+#define __align__(n) __attribute__((aligned(n)))
+
+// ---- vector types -------------------------------------------------------------
+struct dim3 {
+    unsigned x, y, z;
+    constexpr dim3(unsigned x_ = 1, unsigned y_ = 1, unsigned z_ = 1) : x(x_), y(y_), z(z_) {}
+};
+struct alignas(16) float4 { float x, y, z, w; };
+struct alignas(8) float2 { float x, y; };
+struct alignas(8) uint2 { unsigned x, y; };
+inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
+
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }
+
+inline unsigned __float_as_uint(float f) { unsigned u; std::memcpy(&u, &f, 4); return u; }
+inline int __float_as_int(float f) { int u; std::memcpy(&u, &f, 4); return u; }
+inline float __uint_as_float(unsigned u) { float f; std::memcpy(&f, &u, 4); return f; }
+inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; }
+
+// ---- runtime API subset ------------------------------------------------------
+typedef int hipError_t;
+enum {
+    hipSuccess = 0,
+    hipErrorInvalidValue = 1,
+    hipErrorInvalidDevice = 101,
+    hipErrorInvalidSymbol = 13,
+};
+typedef void *hipStream_t;
+typedef void *hipEvent_t;
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 0 };
+#define HIP_SYMBOL(x) (&(x))
+
+inline hipError_t hipGetLastError() { return hipSuccess; }
+inline hipError_t hipGetDevice(int *d) { *d = 0; return hipSuccess; }
+inline hipError_t hipDeviceGetAttribute(int *v, hipDeviceAttribute_t, int) { *v = 256; return hipSuccess; }
+template <typename K>
+hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int *n, K, int, size_t) { *n = 2; return hipSuccess; }
+inline hipError_t hipGetSymbolAddress(void **p, const void *sym) { *p = const_cast<void *>(sym); return hipSuccess; }
+
+// ---- the emulated machine ------------------------------------------------------
+// One fiber (ucontext) per thread of the workgroup, all on the calling OS
+// thread: a barrier parks the fiber and the scheduler resumes the next
+// runnable one in order.  Deterministic, and no OS-thread contention.
+namespace hostemu {
+
+[[noreturn]] inline void fail(const char *what) {
+    std::fprintf(stderr, "hostemu: %s\n", what);
+    std::fflush(stderr);
+    std::abort();
+}
+
+struct Fiber {
+    ucontext_t ctx;
+    char *stack = nullptr;
+    size_t stack_size = 0;
+    void *fake_stack = nullptr;
+    dim3 tid;
+    int lane = 0, wave = 0;
+    bool blocked = false, done = false;
+};
+
+// A barrier over n fibers: the last to arrive releases the others.
+struct Barrier {
+    int n = 0;
+    std::vector<Fiber *> waiting;
+    void wait();
+};
+
+struct Wave {
+    Barrier bar;
+    uint32_t a[64], b[64];
+};
+
+struct Machine {
+    std::vector<Fiber> fibers;
+    Barrier block;
+    std::vector<Wave> waves;
+    Fiber *current = nullptr;
+    ucontext_t sched;
+    void *sched_fake = nullptr;
+    const void *sched_bottom = nullptr;
+    size_t sched_size = 0;
+    std::function<void()> body;
+};
+
+inline Machine *&machine() { static Machine *m = nullptr; return m; }
+inline int t_lane = 0, t_wave = 0;
+
+// Switches from the running fiber back to the scheduler.
+inline void yield_to_scheduler(bool dying) {
+    Machine &m = *machine();
+    Fiber *f = m.current;
+#if defined(__SANITIZE_ADDRESS__)
+    __sanitizer_start_switch_fiber(dying ? nullptr : &f->fake_stack, m.sched_bottom, m.sched_size);
+#else
+    (void)dying;
+#endif
+    swapcontext(&f->ctx, &m.sched);
+#if defined(__SANITIZE_ADDRESS__)
+    __sanitizer_finish_switch_fiber(f->fake_stack, nullptr, nullptr);
+#endif
+}
+
+inline void Barrier::wait() {
+    Machine &m = *machine();
+    if ((int)waiting.size() + 1 == n) {
+        for (Fiber *f : waiting) f->blocked = false;
+        waiting.clear();
+        return;
+    }
+    m.current->blocked = true;
+    waiting.push_back(m.current);
+    yield_to_scheduler(false);
+}
+
+// Every lane publishes (x, y); each returns the pair published by lane src.
+inline void exchange(uint32_t x, uint32_t y, int src, uint32_t *rx, uint32_t *ry) {
+    Wave &w = machine()->waves[t_wave];
+    w.a[t_lane] = x;
+    w.b[t_lane] = y;
+    w.bar.wait();
+    if (src < 0 || src >= 64) fail("cross-lane source lane out of range");
+    *rx = w.a[src];
+    *ry = w.b[src];
+    w.bar.wait();
+}
+
+}  // namespace hostemu
+
+inline dim3 threadIdx, blockIdx;
+inline void __syncthreads() { hostemu::machine()->block.wait(); }
+
+// ---- cross-lane builtins ---------------------------------------------------------
+// DPP (row = 16 lanes): quad_perm 0x00-0xff, row_mirror 0x140, row_half_mirror 0x141.
+inline int hostemu_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
+    const int l = hostemu::t_lane;
+    int from;
+    if (ctrl >= 0 && ctrl <= 0xff) from = (l & ~3) + ((ctrl >> (2 * (l & 3))) & 3);
+    else if (ctrl == 0x140) from = (l & ~15) + (15 - (l & 15));
+    else if (ctrl == 0x141) from = (l & ~7) + (7 - (l & 7));
+    else hostemu::fail("DPP control not emulated");
+    (void)bound_ctrl;
+    uint32_t r, unused;
+    hostemu::exchange((uint32_t)src, 0, from, &r, &unused);
+    const bool enabled = ((row_mask >> (l >> 4)) & 1) && ((bank_mask >> ((l >> 2) & 3)) & 1);
+    return enabled ? (int)r : old;
+}
+#define __builtin_amdgcn_update_dpp hostemu_update_dpp
+
+// V_PERMLANE32_SWAP_B32 vdst, vsrc: lanes 32-63 of vdst swap with lanes 0-31
+// of vsrc.  Returns {new vdst, new vsrc}.
+inline std::array<uint32_t, 2> hostemu_permlane32_swap(uint32_t vdst, uint32_t vsrc, bool, bool) {
+    const int l = hostemu::t_lane;
+    uint32_t d, s;
+    if (l < 32) {
+        uint32_t hi_d, unused;
+        hostemu::exchange(vdst, vsrc, l + 32, &hi_d, &unused);  // vsrc_new[l] = vdst[l + 32]
+        d = vdst;
+        s = hi_d;
+    } else {
+        uint32_t unused, lo_s;
+        hostemu::exchange(vdst, vsrc, l - 32, &unused, &lo_s);  // vdst_new[l] = vsrc[l - 32]
+        d = lo_s;
+        s = vsrc;
+    }
+    return {d, s};
+}
+// V_PERMLANE16_SWAP_B32 vdst, vsrc: odd rows of vdst swap with even rows of
+// vsrc (row = 16 lanes).
+inline std::array<uint32_t, 2> hostemu_permlane16_swap(uint32_t vdst, uint32_t vsrc, bool, bool) {
+    const int l = hostemu::t_lane;
+    uint32_t d, s;
+    if (((l >> 4) & 1) == 0) {
+        uint32_t odd_d, unused;
+        hostemu::exchange(vdst, vsrc, l + 16, &odd_d, &unused);  // vsrc_new[l] = vdst[l + 16]
+        d = vdst;
+        s = odd_d;
+    } else {
+        uint32_t unused, even_s;
+        hostemu::exchange(vdst, vsrc, l - 16, &unused, &even_s);  // vdst_new[l] = vsrc[l - 16]
+        d = even_s;
+        s = vsrc;
+    }
+    return {d, s};
+}
+#define __builtin_amdgcn_permlane32_swap hostemu_permlane32_swap
+#define __builtin_amdgcn_permlane16_swap hostemu_permlane16_swap
+
+inline float __shfl_xor(float v, int mask, int width = 64) {
+    if (width != 64) hostemu::fail("__shfl_xor width other than 64 not emulated");
+    uint32_t r, unused;
+    hostemu::exchange(__float_as_uint(v), 0, hostemu::t_lane ^ mask, &r, &unused);
+    return __uint_as_float(r);
+}
+
+inline float hostemu_exp2f(float x) { return exp2f(x); }
+#define __builtin_amdgcn_exp2f hostemu_exp2f
+
+// ---- buffer resources ------------------------------------------------------------
+struct __amdgpu_buffer_rsrc_t {
+    const char *base;
+    uint32_t num_records;
+};
+inline __amdgpu_buffer_rsrc_t hostemu_make_buffer_rsrc(void *base, short stride, int num_records, int flags) {
+    if (stride != 0) hostemu::fail("strided buffer descriptor not emulated");
+    (void)flags;
+    return __amdgpu_buffer_rsrc_t{static_cast<const char *>(base), (uint32_t)num_records};
+}
+inline std::array<uint32_t, 4> hostemu_raw_buffer_load_b128(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff,
+                                                           int aux) {
+    (void)aux;
+    const uint64_t off = (uint64_t)voff + soff;
+    if (off + 16 > r.num_records) hostemu::fail("buffer load beyond num_records");
+    std::array<uint32_t, 4> v;
+    std::memcpy(v.data(), r.base + off, 16);
+    return v;
+}
+#define __builtin_amdgcn_make_buffer_rsrc hostemu_make_buffer_rsrc
+#define __builtin_amdgcn_raw_buffer_load_b128 hostemu_raw_buffer_load_b128
+
+// ---- launches ------------------------------------------------------------------------
+namespace hostemu {
+
+inline void fiber_entry() {
+    Machine &m = *machine();
+#if defined(__SANITIZE_ADDRESS__)
+    __sanitizer_finish_switch_fiber(nullptr, &m.sched_bottom, &m.sched_size);
+#endif
+    m.body();
+    m.current->done = true;
+    yield_to_scheduler(true);
+    fail("finished fiber resumed");
+}
+
+// Runs every workgroup of `grid` in order on one team of blockDim fibers.
+template <typename K, typename... A>
+void launch(K kernel, dim3 grid, dim3 block, A... args) {
+    const int nt = (int)(block.x * block.y * block.z);
+    if (nt % 64) fail("workgroup size not a multiple of 64");
+    Machine m;
+    machine() = &m;
+    m.fibers = std::vector<Fiber>(nt);
+    m.block.n = nt;
+    m.waves = std::vector<Wave>(nt / 64);
+    for (auto &w : m.waves) w.bar.n = 64;
+    m.body = [&] {
+        for (unsigned z = 0; z < grid.z; z++)
+            for (unsigned y = 0; y < grid.y; y++)
+                for (unsigned x = 0; x < grid.x; x++) {
+                    blockIdx = dim3(x, y, z);
+                    kernel(args...);
+                    __syncthreads();  // the workgroup has ended before the next one starts
+                }
+    };
+    const size_t stack_size = (size_t)1 << 17;
+    for (int i = 0; i < nt; i++) {
+        Fiber &f = m.fibers[i];
+        f.tid = dim3(i % block.x, (i / block.x) % block.y, i / (block.x * block.y));
+        f.lane = i & 63;
+        f.wave = i >> 6;
+        f.stack = static_cast<char *>(std::malloc(stack_size));
+        f.stack_size = stack_size;
+        if (!f.stack || getcontext(&f.ctx)) fail("fiber setup");
+        f.ctx.uc_stack.ss_sp = f.stack;
+        f.ctx.uc_stack.ss_size = stack_size;
+        f.ctx.uc_link = nullptr;
+        makecontext(&f.ctx, fiber_entry, 0);
+    }
+    for (int left = nt; left > 0;) {
+        bool ran = false;
+        for (auto &f : m.fibers) {
+            if (f.done || f.blocked) continue;
+            ran = true;
+            m.current = &f;
+            threadIdx = f.tid;
+            t_lane = f.lane;
+            t_wave = f.wave;
+#if defined(__SANITIZE_ADDRESS__)
+            __sanitizer_start_switch_fiber(&m.sched_fake, f.stack, f.stack_size);
+#endif
+            swapcontext(&m.sched, &f.ctx);
+#if defined(__SANITIZE_ADDRESS__)
+            __sanitizer_finish_switch_fiber(m.sched_fake, nullptr, nullptr);
+#endif
+            if (f.done) left--;
+        }
+        if (!ran && left > 0) fail("deadlock: a barrier or cross-lane operation not reached by every lane");
+    }
+    for (auto &f : m.fibers) std::free(f.stack);
+    machine() = nullptr;
+}
+
+}  // namespace hostemu
+
+#define hipLaunchKernelGGL(kernel, grid, block, shmem, stream, ...) \
+    hostemu::launch(kernel, dim3(grid), dim3(block), __VA_ARGS__)
+
+#endif

@@ -176,8 +176,24 @@ typedef struct {
     /* 0: y[m] = A[m] . x.  G3K_MV_GEGLU: n_mat = 2, M[0] == M[1],
      * y[0] = gelu_tanh(A[0] . x) * (A[1] . x)  (gemma3_transformer.c:380-386) */
     int mode;
+    /* Residual prologue, taken when pre_t is set (K <= G3K_MATVEC_PRE_MAX).
+     * x is then not read: every workgroup forms it in LDS from the step that
+     * sits between two GEMVs of the token forward (gemma3_transformer.c:
+     * 463-477, 490-496, 444-446):
+     *   s = pre_r + rmsnorm(pre_t, pre_w_post)    (pre_r + pre_t without pre_w_post)
+     *   x = rmsnorm(s, pre_w_next)                (s without pre_w_next)
+     * with rmsnorm as gemma3_rmsnorm_bf16 (gemma3_kernels.c:289-304) at
+     * pre_eps, and workgroup 0 stores s to pre_r_out.  pre_r_out must not
+     * overlap pre_r: the other workgroups read pre_r while it is written.
+     * K % 4 == 0; pre_t, pre_r and pre_r_out 16-byte aligned, the gain rows
+     * 8-byte aligned. */
+    const float *pre_t, *pre_r;
+    const uint16_t *pre_w_post, *pre_w_next;
+    float *pre_r_out;
+    float pre_eps;
 } g3k_matvec_args;
 #define G3K_MV_GEGLU 1
+#define G3K_MATVEC_PRE_MAX 4096
 
 int g3k_matvec(const g3k_matvec_args *a, void *stream);
 

@@ -148,6 +148,10 @@ struct g3attn_ctx {
     int n_cu;       /* compute units of the device */
     /* decode: non-temporal cache loads (G3ATTN_DECODE_NT=0 turns them off) */
     int nt_loads;
+    /* token forward: residual steps folded into the next GEMV's prologue
+     * (bit 0: into the Q/K/V launch, bit 1: into the gate/up launch;
+     * G3ATTN_FORWARD_FOLD) */
+    int forward_fold;
 };
 
 static void prof_destroy(g3attn_ctx *c) {
@@ -308,6 +312,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         c->prefill_sched = sch ? atoi(sch) : 1;
         const char *nt = getenv("G3ATTN_DECODE_NT");
         c->nt_loads = nt ? atoi(nt) != 0 : 1;
+        const char *ff = getenv("G3ATTN_FORWARD_FOLD");
+        c->forward_fold = ff ? atoi(ff) & 3 : 1;
         if (c->min_rows < G3K_SPLIT_GRAIN) c->min_rows = G3K_SPLIT_GRAIN;
     }
 
@@ -1145,14 +1151,38 @@ static int forward_check(g3attn_ctx *c, const g3attn_weights *w, int token_id, i
 static int forward_buffers(g3attn_ctx *c) {
     const g3attn_config *cfg = &c->cfg;
     const size_t hb = align256((size_t)cfg->hidden_size * 4);
-    int rc = grow_buf(c, &c->d_fw, &c->d_fw_cap, 4 * hb + align256((size_t)cfg->intermediate_size * 4),
+    int rc = grow_buf(c, &c->d_fw, &c->d_fw_cap, 5 * hb + align256((size_t)cfg->intermediate_size * 4),
                       "forward activations");
     if (rc) return rc;
     const int qs = cfg->num_heads * D, ks = cfg->num_kv_heads * D;
     return grow_buf(c, &c->d_la, &c->d_la_cap, (size_t)(2 * qs + 2 * ks) * sizeof(float), "layer scratch");
 }
 
-/* Enqueue one token of gemma3_transformer_forward (:396-512). */
+/* A GEMV whose x is formed by the residual prologue (g3k_matvec_args.pre_*):
+ * s = *x + rmsnorm(t, w_post) goes to *x_alt, and the two residual buffers
+ * swap. */
+static void set_pre(g3k_matvec_args *a, const g3attn_config *cfg, float **x, float **x_alt, const float *t,
+                    const uint16_t *w_post, const uint16_t *w_next) {
+    a->pre_t = t;
+    a->pre_r = *x;
+    a->pre_r_out = *x_alt;
+    a->pre_w_post = w_post;
+    a->pre_w_next = w_next;
+    a->pre_eps = cfg->rmsnorm_eps;
+    float *tmp = *x;
+    *x = *x_alt;
+    *x_alt = tmp;
+}
+
+/* Enqueue one token of gemma3_transformer_forward (:396-512).
+ *
+ * The residual step between two GEMVs (post-norm, residual add, the next
+ * pre-norm) is folded into the prologue of the GEMV that consumes it where
+ * c->forward_fold allows and the hidden size fits the prologue: the Q/K/V
+ * launch of the next layer, and the gate/up launch.  The residual stream
+ * then alternates between two buffers (x, x_alt), since every workgroup of
+ * the folded launch reads the old residual while workgroup 0 writes the new
+ * one.  Otherwise the one-workgroup residual_kernel runs in between. */
 static int forward_enqueue(g3attn_ctx *c, const g3attn_weights *w, int token_id, int pos, float *logits,
                            int compute_logits, float *hidden_out) {
     const g3attn_config *cfg = &c->cfg;
@@ -1161,27 +1191,50 @@ static int forward_enqueue(g3attn_ctx *c, const g3attn_weights *w, int token_id,
     const int qs = cfg->num_heads * D, ks = cfg->num_kv_heads * D;
     unsigned char *b = (unsigned char *)c->d_fw;
     float *x = (float *)b, *xn = (float *)(b + hb), *proj = (float *)(b + 2 * hb);
-    float *mlp = (float *)(b + 3 * hb), *h = (float *)(b + 4 * hb);
+    float *mlp = (float *)(b + 3 * hb), *x_alt = (float *)(b + 4 * hb), *h = (float *)(b + 5 * hb);
     float *q = c->d_la, *k = q + qs, *v = k + ks, *attn = v + ks;
+    const int can_fold = hid <= G3K_MATVEC_PRE_MAX && hid % 4 == 0;
+    const int fold_qkv = can_fold && (c->forward_fold & 1), fold_mlp = can_fold && (c->forward_fold & 2);
     int rc;
+    /* the prologue reads gain rows as 8-byte words: a step whose gains sit at
+     * other offsets (weights mapped from a file as is) runs unfolded */
+#define AL8(p) (((uintptr_t)(p) & 7) == 0)
 
     /* embedding * sqrt(hidden) (:415-422), then layer 0's input norm (:444-446) */
     if ((rc = layer_step(c, G3K_OP_EMBED, x, NULL, NULL, NULL, NULL, w->embed_tokens, token_id))) return rc;
     if ((rc = layer_step(c, G3K_OP_NORM, x, NULL, xn, NULL, w->layers[0].input_layernorm, NULL, 0))) return rc;
     for (int l = 0; l < L; l++) {
         const g3attn_layer_weights *lw = &w->layers[l];
-        /* layer_attention (:449-460) */
-        if ((rc = g3attn_qkv_proj_device(c, xn, lw->q_proj, lw->k_proj, lw->v_proj, q, k, v))) return rc;
+        /* layer_attention (:449-460); with fold_qkv (l > 0) the previous
+         * layer's post-feedforward norm, residual add and this layer's input
+         * norm (:490-496, 444-446) run in the Q/K/V launch's prologue */
+        if (fold_qkv && l > 0 && AL8(w->layers[l - 1].post_feedforward_layernorm) &&
+            AL8(lw->input_layernorm)) {
+            g3k_matvec_args a;
+            memset(&a, 0, sizeof a);
+            a.K = hid;
+            a.n_mat = 3;
+            a.A[0] = lw->q_proj;
+            a.y[0] = q;
+            a.M[0] = qs;
+            a.A[1] = lw->k_proj;
+            a.y[1] = k;
+            a.M[1] = ks;
+            a.A[2] = lw->v_proj;
+            a.y[2] = v;
+            a.M[2] = ks;
+            set_pre(&a, cfg, &x, &x_alt, mlp, w->layers[l - 1].post_feedforward_layernorm, lw->input_layernorm);
+            if ((rc = g3k_matvec(&a, c->stream))) return hip_fail((hipError_t)rc, "g3attn_forward_device Q/K/V");
+        } else if ((rc = g3attn_qkv_proj_device(c, xn, lw->q_proj, lw->k_proj, lw->v_proj, q, k, v))) {
+            return rc;
+        }
         if ((rc = g3attn_decode_device(c, l, pos, q, k, v, lw->q_norm, lw->k_norm, attn))) return rc;
         if ((rc = gemv(c, proj, lw->o_proj, attn, hid, qs))) return rc;
-        /* post-attention norm, residual, pre-feedforward norm (:463-477) */
-        if ((rc = layer_step(c, G3K_OP_RESIDUAL, x, proj, xn, lw->post_attention_layernorm,
-                             lw->pre_feedforward_layernorm, NULL, 0)))
-            return rc;
-        /* layer_mlp (:480-487, 369-388): gate and up GEMVs with gelu(gate) * up, down GEMV */
+        /* layer_mlp (:480-487, 369-388): gate and up GEMVs with gelu(gate) * up,
+         * after the post-attention norm, residual add and pre-feedforward
+         * norm (:463-477), folded into the launch's prologue with fold_mlp */
         g3k_matvec_args a;
         memset(&a, 0, sizeof a);
-        a.x = xn;
         a.K = hid;
         a.n_mat = 2;
         a.mode = G3K_MV_GEGLU;
@@ -1189,16 +1242,28 @@ static int forward_enqueue(g3attn_ctx *c, const g3attn_weights *w, int token_id,
         a.A[1] = lw->up_proj;
         a.y[0] = h;
         a.M[0] = a.M[1] = inter;
+        if (fold_mlp && AL8(lw->post_attention_layernorm) && AL8(lw->pre_feedforward_layernorm)) {
+            set_pre(&a, cfg, &x, &x_alt, proj, lw->post_attention_layernorm, lw->pre_feedforward_layernorm);
+        } else {
+            if ((rc = layer_step(c, G3K_OP_RESIDUAL, x, proj, xn, lw->post_attention_layernorm,
+                                 lw->pre_feedforward_layernorm, NULL, 0)))
+                return rc;
+            a.x = xn;
+        }
         if ((rc = g3k_matvec(&a, c->stream))) return hip_fail((hipError_t)rc, "g3attn_forward_device MLP");
         if ((rc = gemv(c, mlp, lw->down_proj, h, hid, inter))) return rc;
         /* post-feedforward norm, residual (:490-496); then the next layer's
-         * input norm, or the final norm before the logits (:508) */
+         * input norm (folded into its Q/K/V launch with fold_qkv), or the
+         * final norm before the logits (:508) */
         const int last = l + 1 == L;
+        if (!last && fold_qkv && AL8(lw->post_feedforward_layernorm) && AL8(w->layers[l + 1].input_layernorm))
+            continue;
         const uint16_t *w_next = last ? (compute_logits ? w->norm : NULL) : w->layers[l + 1].input_layernorm;
         if ((rc = layer_step(c, G3K_OP_RESIDUAL, x, mlp, (last && !compute_logits) ? NULL : xn,
                              lw->post_feedforward_layernorm, w_next, NULL, 0)))
             return rc;
     }
+#undef AL8
     /* tied-embedding logits (:511) */
     if (compute_logits && (rc = gemv(c, logits, w->embed_tokens, xn, cfg->vocab_size, hid))) return rc;
     if (hidden_out)

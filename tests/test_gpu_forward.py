@@ -86,6 +86,32 @@ def test_forward_matches_reference_golden():
         assert rel_err(logits[i], want[i]) < 1e-4, i
 
 
+@pytest.mark.parametrize("fold", [0, 1, 3])
+def test_forward_fold_modes(fold, monkeypatch):
+    """The residual step between two GEMVs (post-norm, residual add, next
+    pre-norm) as the one-workgroup kernel (G3ATTN_FORWARD_FOLD=0), in the
+    prologue of the next layer's Q/K/V launch (1, the default), or also in
+    the gate/up launch's (3): every step's logits and the final hidden state
+    against the oracle.  Layer 2's input norm sits 2 bytes past an 8-byte
+    boundary, so the fold into layer 2's Q/K/V launch falls back to the
+    kernel for that step, and the residual stream still comes out right."""
+    monkeypatch.setenv("G3ATTN_FORWARD_FOLD", str(fold))
+    cfg, f, embed, layers, norm, tokens = MG.forward_case()
+    with G.Context(_gpu_config(f), f["max_context"]) as ctx:
+        W, bufs = _upload(embed, layers, norm)
+        gain = layers[2]["input_layernorm"]
+        odd = DeviceBuffer(gain.nbytes + 16)
+        odd.upload(gain, offset=2)
+        W.layers[2].input_layernorm = odd.ptr + 2
+        rows, hid = _run(ctx, W, tokens, f)
+    want, want_h = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm)
+    errs = [rel_err(rows[i], want[i]) for i in range(len(tokens))]
+    err_h = rel_err(hid, want_h)
+    print(f"[forward fold={fold}] worst logits rel={max(errs):.3e} hidden rel={err_h:.3e}", flush=True)
+    assert max(errs) < 1e-4 and err_h < 1e-4
+    assert np.array_equal(np.stack(rows).argmax(axis=1), want.argmax(axis=1))
+
+
 def test_forward_without_logits_is_identical():
     """compute_logits = 0 skips the final norm and vocab GEMV only: the state
     the next step reads is bit-identical, so the last step's logits are too."""

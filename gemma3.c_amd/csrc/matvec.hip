@@ -342,7 +342,8 @@ extern "C" int g3k_matvec(const g3k_matvec_args *a, void *stream) {
     if (pre && (!a->pre_r || !a->pre_r_out || a->K > G3K_MATVEC_PRE_MAX || a->K % 4 ||
                 (((uintptr_t)a->pre_t | (uintptr_t)a->pre_r | (uintptr_t)a->pre_r_out) & 15) ||
                 (((uintptr_t)a->pre_w_post | (uintptr_t)a->pre_w_next) & 7) ||
-                (a->pre_r_out < a->pre_r + a->K && a->pre_r < a->pre_r_out + a->K)))
+                ((uintptr_t)a->pre_r_out < (uintptr_t)(a->pre_r + a->K) &&
+                 (uintptr_t)a->pre_r < (uintptr_t)(a->pre_r_out + a->K))))
         return (int)hipErrorInvalidValue;
     // with the prologue x comes from LDS, 16-byte aligned
     bool vec = a->K % 8 == 0 && (pre || ((uintptr_t)a->x & 15) == 0);

@@ -153,24 +153,6 @@ __device__ __forceinline__ void load_step(float (&kk)[R][4][4], float (&vv)[R][4
     }
 }
 
-// Write a merged result: normalised output, or an (m, l, acc) partial.
-template <int G>
-__device__ __forceinline__ void emit(const float *s_res, const float *s_resml, float *out,
-                                     float *acc, float *ml) {
-    for (int e = threadIdx.x; e < G * D; e += NT) {
-        const int g = e / D;
-        if (out) {
-            out[e] = s_res[e] / s_resml[g * 2 + 1];
-        } else {
-            acc[e] = s_res[e];
-            if (e % D == 0) {
-                ml[g * 2] = s_resml[g * 2];
-                ml[g * 2 + 1] = s_resml[g * 2 + 1];
-            }
-        }
-    }
-}
-
 // One step: scores of this lane-group's R rows for the G query heads (16-lane
 // DPP reduction), online-softmax update with a wave-uniform running max, and
 // the P.V accumulation.
@@ -254,8 +236,6 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
 
     __shared__ float s_acc[NW][G * D];
     __shared__ float s_m[NW][G], s_l[NW][G];
-    __shared__ float s_res[G * D];
-    __shared__ float s_resml[G * 2];
 
     const float *kbase = p.kc + (size_t)kvh * p.head_stride;
     const float *vbase = p.vc + (size_t)kvh * p.head_stride;
@@ -366,7 +346,12 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     }
     __syncthreads();
 
-    // ---- merge the waves: this workgroup's (m, l, acc) per query head ----
+    // ---- merge the waves: this workgroup's (m, l, acc) per query head, stored
+    // straight from the merging thread (every thread of a head computes the
+    // same M and L): the normalised output with one split, else this split's
+    // partial ----
+    float *out = p.out + (size_t)kvh * G * D;
+    const size_t slot = (size_t)kvh * G3K_MAX_SPLITS + split;
     for (int e = tid; e < G * D; e += NT) {
         const int g = e / D;
         float M = s_m[0][g];
@@ -379,21 +364,16 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
             L += s_l[w][g] * f;
             A += s_acc[w][e] * f;
         }
-        s_res[e] = A;
-        if (e % D == 0) {
-            s_resml[g * 2] = M;
-            s_resml[g * 2 + 1] = L;
+        if (p.n_splits == 1) {   // uniform
+            out[e] = A / L;
+        } else {
+            p.ws_acc[slot * G * D + e] = A;
+            if (e % D == 0) {
+                p.ws_ml[(slot * G + g) * 2] = M;
+                p.ws_ml[(slot * G + g) * 2 + 1] = L;
+            }
         }
     }
-    __syncthreads();
-    float *out = p.out + (size_t)kvh * G * D;
-    if (p.n_splits == 1) {
-        emit<G>(s_res, s_resml, out, nullptr, nullptr);
-        return;
-    }
-    // ---- this split's partial ----
-    const size_t slot = (size_t)kvh * G3K_MAX_SPLITS + split;
-    emit<G>(s_res, s_resml, nullptr, p.ws_acc + slot * G * D, p.ws_ml + slot * G * 2);
 }
 
 // Cross-split combine, one launch after decode_kernel (kernel order makes
@@ -466,7 +446,7 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
     if (tid < 8) {
 #pragma unroll
         for (int w = 1; w < NW; w++) merge_ml(M, L, A, s_m[w][tid], s_l[w][tid], s_a[w][tid]);
-        // a division, as the single-split path's emit: one split gives the same bits either way
+        // a division, as the single-split path's store: one split gives the same bits either way
         *reinterpret_cast<float4 *>(p.out + ((size_t)kvh * G + g) * D + d) =
             make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
     }

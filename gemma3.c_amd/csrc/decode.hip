@@ -227,6 +227,22 @@ __device__ __forceinline__ void merge_ml(float &M, float &L, float4 &A, float m2
     M = Mn;
 }
 
+// (M, L, A) <- the merge of the partials of lanes l and l ^ X (X = 16 or 32),
+// lower lane first, through v_permlane{16,32}_swap.
+template <int X>
+__device__ __forceinline__ void swap_merge(float &M, float &L, float4 &A) {
+    auto sw = [](float v) {
+        const auto r = X == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                               : __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    };
+    const float2 m = sw(M), l = sw(L), ax = sw(A.x), ay = sw(A.y), az = sw(A.z), aw = sw(A.w);
+    M = m.x;
+    L = l.x;
+    A = make_float4(ax.x, ay.x, az.x, aw.x);
+    merge_ml(M, L, A, m.y, l.y, make_float4(ax.y, ay.y, az.y, aw.y));
+}
+
 template <int G, bool FUSED, bool NTL>
 __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     constexpr int R = rows_for<G>();
@@ -424,17 +440,23 @@ __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
         A.z += aq[u].z * b;
         A.w += aq[u].w * b;
     }
-    // the 8 split lanes of this wave: lanes f + 8 k
-#pragma unroll
-    for (int o = 8; o < 64; o <<= 1) {
-        const float m2 = __shfl_xor(M, o), l2 = __shfl_xor(L, o);
+    // the 8 split lanes of this wave: lanes f + 8 k.  Lanes l and l ^ 8 meet
+    // through DPP row_ror:8 (l ^ 8 within a 16-lane row), then l ^ 16 and
+    // l ^ 32 through v_permlane16/32_swap, whose two results hold the lower
+    // lane's partial, then the upper lane's, in both lanes: all VALU, no LDS
+    // round trip.  Lanes 0..7 (the ones stored below) merge (own, partner)
+    // at every level.
+    {
         float4 a2;
-        a2.x = __shfl_xor(A.x, o);
-        a2.y = __shfl_xor(A.y, o);
-        a2.z = __shfl_xor(A.z, o);
-        a2.w = __shfl_xor(A.w, o);
+        const float m2 = dpp<0x128>(M), l2 = dpp<0x128>(L);
+        a2.x = dpp<0x128>(A.x);
+        a2.y = dpp<0x128>(A.y);
+        a2.z = dpp<0x128>(A.z);
+        a2.w = dpp<0x128>(A.w);
         merge_ml(M, L, A, m2, l2, a2);
     }
+    swap_merge<16>(M, L, A);
+    swap_merge<32>(M, L, A);
     __shared__ float s_m[NW][8], s_l[NW][8];
     __shared__ float4 s_a[NW][8];
     if (lane < 8) {

@@ -58,6 +58,7 @@ struct alignas(16) float4 { float x, y, z, w; };
 struct alignas(8) float2 { float x, y; };
 struct alignas(8) uint2 { unsigned x, y; };
 inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
+inline float2 make_float2(float x, float y) { return float2{x, y}; }
 
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
@@ -181,11 +182,13 @@ inline dim3 threadIdx, blockIdx;
 inline void __syncthreads() { hostemu::machine()->block.wait(); }
 
 // ---- cross-lane builtins ---------------------------------------------------------
-// DPP (row = 16 lanes): quad_perm 0x00-0xff, row_mirror 0x140, row_half_mirror 0x141.
+// DPP (row = 16 lanes): quad_perm 0x00-0xff, row_ror:8 0x128 (lane i reads
+// lane i ^ 8 of its row), row_mirror 0x140, row_half_mirror 0x141.
 inline int hostemu_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool bound_ctrl) {
     const int l = hostemu::t_lane;
     int from;
     if (ctrl >= 0 && ctrl <= 0xff) from = (l & ~3) + ((ctrl >> (2 * (l & 3))) & 3);
+    else if (ctrl == 0x128) from = l ^ 8;
     else if (ctrl == 0x140) from = (l & ~15) + (15 - (l & 15));
     else if (ctrl == 0x141) from = (l & ~7) + (7 - (l & 7));
     else hostemu::fail("DPP control not emulated");

@@ -268,7 +268,14 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
                                              int tok, int qhead, int n_heads, int g) {
     const bool qv = tok < p.n;
     const float *qrow = p.q + ((size_t)(qv ? tok : 0) * n_heads + qhead) * D + 8 * g;
+    const float *rrow = p.rope + (size_t)(p.start_pos + (qv ? tok : 0)) * D + 2 * 8 * g;
+    // Every load of the prologue is issued before the first use: the query
+    // row, the norm gains and the RoPE table row come back in one memory
+    // round trip.  (Without q_norm the gain load reads a valid row of the
+    // table and its values are not used: no branch between the loads.)
     float x[8][8];
+    uint4 wv[8];
+    float4 cs[4][4];
 #pragma unroll
     for (int t = 0; t < 8; t++) {
         const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * t);
@@ -276,6 +283,16 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
         x[t][0] = a.x; x[t][1] = a.y; x[t][2] = a.z; x[t][3] = a.w;
         x[t][4] = b.x; x[t][5] = b.y; x[t][6] = b.z; x[t][7] = b.w;
     }
+    const uint16_t *wrow = p.q_norm ? p.q_norm : reinterpret_cast<const uint16_t *>(p.rope);
+#pragma unroll
+    for (int t = 0; t < 8; t++) wv[t] = *reinterpret_cast<const uint4 *>(wrow + 32 * t + 8 * g);
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int h = 0; h < 4; h++) cs[t][h] = *reinterpret_cast<const float4 *>(rrow + 64 * t + 4 * h);
+    // keep the scheduler from sinking the gain and table loads below the
+    // query row's waits (which would make them further round trips)
+    __builtin_amdgcn_sched_barrier(0);
     if (p.q_norm) {
         float ss = 0.f;
 #pragma unroll
@@ -286,20 +303,17 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
         const float r = 1.0f / sqrtf(ss / (float)D + p.eps);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const uint4 wv = *reinterpret_cast<const uint4 *>(p.q_norm + 32 * t + 8 * g);
-            const uint32_t w[4] = {wv.x, wv.y, wv.z, wv.w};
+            const uint32_t w[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
 #pragma unroll
             for (int u = 0; u < 8; u++)
                 x[t][u] = x[t][u] * r * (1.0f + bf16f((w[u >> 1] >> (16 * (u & 1))) & 0xffff));
         }
     }
-    const float *rrow = p.rope + (size_t)(p.start_pos + (qv ? tok : 0)) * D + 2 * 8 * g;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
 #pragma unroll
         for (int h = 0; h < 4; h++) {
-            const float4 cs = *reinterpret_cast<const float4 *>(rrow + 64 * t + 4 * h);
-            const float c[2] = {cs.x, cs.z}, sn[2] = {cs.y, cs.w};
+            const float c[2] = {cs[t][h].x, cs[t][h].z}, sn[2] = {cs[t][h].y, cs[t][h].w};
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const int u = 2 * h + e;

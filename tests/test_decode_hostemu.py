@@ -2,10 +2,11 @@
 
 tests/hostemu/Makefile compiles gemma3.c_amd/csrc/decode.hip (decode_kernel,
 combine_kernel and the g3k_decode launcher, unchanged) as host C++ against
-stand-in HIP headers that emulate a wave64 machine on threads: cross-lane
-DPP / permlane-swap / shuffle exchanges between barriers, __syncthreads over
-the workgroup, and buffer loads that abort when they leave their descriptor's
-range.  Every input and output is its own exact-size heap allocation.  The
+stand-in HIP headers that emulate a wave64 machine on host fibers (one
+ucontext per GPU thread): cross-lane DPP / permlane-swap / shuffle exchanges
+between barriers, __syncthreads over the workgroup, and buffer loads that
+abort when they leave their descriptor's range.  The cross-lane lane layouts
+were checked against gfx950 with an in-bounds probe of the builtins.  Every input and output is its own exact-size heap allocation.  The
 builds stop at the first sanitizer report.
 
 What this shows, for the cases below: no out-of-range access, no undefined

@@ -1,7 +1,8 @@
-// hip/hip_runtime.h for the host-emulation build of the decode kernels.
+// hip/hip_runtime.h for the host-emulation builds of the decode and GEMV kernels.
 //
 // TEST INFRASTRUCTURE.  tests/hostemu/Makefile compiles
-// gemma3.c_amd/csrc/decode.hip as plain C++ (g++, -fsanitize=address,undefined)
+// gemma3.c_amd/csrc/decode.hip and matvec.hip as plain C++ (g++,
+// -fsanitize=address,undefined)
 // with this directory first on the include path, so the kernels' own source
 // runs on the CPU under the sanitizers.  This header supplies the subset of
 // the HIP device language those kernels use, emulated on the host:
@@ -57,6 +58,8 @@ struct dim3 {
 struct alignas(16) float4 { float x, y, z, w; };
 struct alignas(8) float2 { float x, y; };
 struct alignas(8) uint2 { unsigned x, y; };
+struct alignas(16) uint4 { unsigned x, y, z, w; };
+inline uint4 make_uint4(unsigned x, unsigned y, unsigned z, unsigned w) { return uint4{x, y, z, w}; }
 inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
 inline float2 make_float2(float x, float y) { return float2{x, y}; }
 

@@ -5,6 +5,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Waits until every vector-memory operation this wave issued has completed,
+// buffer -> LDS fetches included.  An asm statement with a memory clobber,
+// so it also keeps the compiler from moving memory accesses across it.  The
+// host-emulation build (tests/hostemu), whose loads complete when issued,
+// defines it away before this header.
+#ifndef G3K_WAIT_VMEM
+#define G3K_WAIT_VMEM() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
+#endif
+
 namespace g3k {
 
 template <int CTRL>

@@ -211,7 +211,7 @@ __device__ __forceinline__ void fetch_v(unsigned char *dst, __amdgpu_buffer_rsrc
 
 // Wait until this wave's buffer->LDS fetches have landed (vmcnt counts them;
 // nothing else is outstanding in the loop).
-__device__ __forceinline__ void wait_fetch_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void wait_fetch_all() { G3K_WAIT_VMEM(); }
 
 // Keeps the compiler's scheduler from moving instructions across this point:
 // used to hold fragment reads one step ahead of the MFMAs that consume them.

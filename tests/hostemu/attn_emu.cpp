@@ -1,0 +1,202 @@
+// attn_emu.cpp - runs a script of g3attn C-ABI calls against the whole
+// library (gemma3.c_amd/host + csrc) built for the emulated GPU of
+// hip/hip_runtime.h, under AddressSanitizer + UndefinedBehaviorSanitizer.
+// TEST INFRASTRUCTURE.
+//
+//   attn_emu <dir>
+//
+// <dir>/script.txt holds one call per line; file names are relative to <dir>
+// (raw little-endian arrays; "-" for an absent optional one).  Any nonzero
+// return stops the run with exit status 1 and the library's error text.
+//
+//   create H Hkv max_context window num_layers eps rope_local rope_global
+//   kv_write layer slot n k v                  (rows [n][Hkv][256])
+//   kv_read layer slot n k_out v_out
+//   prefill layer start_pos n Q K V q_norm k_norm out
+//   prefill_device ...                          (same, device pointers)
+//   decode layer pos q k v q_norm k_norm out
+//   matmul N M K W X C                          (g3attn_matmul_bf16_device)
+//   destroy
+//
+// At the end it prints "launch <kernel> <count>" for every kernel launched
+// and "attn_emu: ok".
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include <hip/hip_runtime_api.h>
+
+#include "g3attn.h"
+
+namespace {
+
+std::string g_dir;
+
+[[noreturn]] void die(const std::string &what) {
+    std::fprintf(stderr, "attn_emu: %s\n", what.c_str());
+    std::exit(2);
+}
+
+template <typename T>
+std::vector<T> read_bin(const std::string &name, size_t n) {
+    std::vector<T> v(n);
+    FILE *f = std::fopen((g_dir + "/" + name).c_str(), "rb");
+    if (!f || std::fread(v.data(), sizeof(T), n, f) != n) die("cannot read " + std::to_string(n) + " values from " + name);
+    std::fclose(f);
+    return v;
+}
+
+template <typename T>
+void write_bin(const std::string &name, const T *p, size_t n) {
+    FILE *f = std::fopen((g_dir + "/" + name).c_str(), "wb");
+    if (!f || std::fwrite(p, sizeof(T), n, f) != n) die("cannot write " + name);
+    std::fclose(f);
+}
+
+// An optional bf16 row of 256 gains: "-" is NULL.
+struct Gain {
+    std::vector<uint16_t> v;
+    const uint16_t *ptr() const { return v.empty() ? nullptr : v.data(); }
+};
+Gain read_gain(const std::string &name) {
+    Gain g;
+    if (name != "-") g.v = read_bin<uint16_t>(name, 256);
+    return g;
+}
+
+// A device copy of a host array (emulated device memory: its own heap block).
+template <typename T>
+T *to_device(const std::vector<T> &h) {
+    void *d = nullptr;
+    if (hipMalloc(&d, h.size() * sizeof(T)) != hipSuccess) die("hipMalloc");
+    hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice);
+    return static_cast<T *>(d);
+}
+
+void check(int rc, const std::string &call) {
+    if (rc) {
+        std::fprintf(stderr, "attn_emu: %s returned %d: %s\n", call.c_str(), rc, g3attn_last_error());
+        std::exit(1);
+    }
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc != 2) die("usage: attn_emu <dir>");
+    g_dir = argv[1];
+    std::ifstream script(g_dir + "/script.txt");
+    if (!script) die("no script.txt");
+    g3attn_ctx *ctx = nullptr;
+    int H = 0, Hkv = 0;
+    const size_t D = 256;
+    std::string line;
+    while (std::getline(script, line)) {
+        std::istringstream in(line);
+        std::string cmd;
+        if (!(in >> cmd) || cmd[0] == '#') continue;
+        if (cmd == "create") {
+            int max_ctx, window, layers;
+            float eps;
+            std::string rl, rg;
+            in >> H >> Hkv >> max_ctx >> window >> layers >> eps >> rl >> rg;
+            if (!in) die("bad create line");
+            g3attn_config cfg;
+            g3attn_default_config(&cfg);
+            cfg.num_heads = H;
+            cfg.num_kv_heads = Hkv;
+            cfg.max_context = max_ctx;
+            cfg.sliding_window = window;
+            cfg.num_layers = layers;
+            cfg.rmsnorm_eps = eps;
+            const auto tl = read_bin<float>(rl, (size_t)max_ctx * D);
+            const auto tg = read_bin<float>(rg, (size_t)max_ctx * D);
+            ctx = g3attn_create(&cfg, max_ctx, tl.data(), tg.data());
+            if (!ctx) {
+                std::fprintf(stderr, "attn_emu: g3attn_create failed: %s\n", g3attn_last_error());
+                return 1;
+            }
+        } else if (cmd == "kv_write" || cmd == "kv_read") {
+            int layer, slot, n;
+            std::string kf, vf;
+            in >> layer >> slot >> n >> kf >> vf;
+            if (!in || !ctx) die("bad " + cmd + " line");
+            const size_t cnt = (size_t)n * Hkv * D;
+            if (cmd == "kv_write") {
+                const auto k = read_bin<float>(kf, cnt), v = read_bin<float>(vf, cnt);
+                check(g3attn_kv_write(ctx, layer, slot, n, k.data(), v.data()), cmd);
+            } else {
+                std::vector<float> k(cnt), v(cnt);
+                check(g3attn_kv_read(ctx, layer, slot, n, k.data(), v.data()), cmd);
+                write_bin(kf, k.data(), cnt);
+                write_bin(vf, v.data(), cnt);
+            }
+        } else if (cmd == "prefill" || cmd == "prefill_device") {
+            int layer, start, n;
+            std::string qf, kf, vf, qn, kn, of;
+            in >> layer >> start >> n >> qf >> kf >> vf >> qn >> kn >> of;
+            if (!in || !ctx) die("bad prefill line");
+            const auto Q = read_bin<float>(qf, (size_t)n * H * D);
+            const auto K = read_bin<float>(kf, (size_t)n * Hkv * D);
+            const auto V = read_bin<float>(vf, (size_t)n * Hkv * D);
+            const Gain gq = read_gain(qn), gk = read_gain(kn);
+            std::vector<float> out((size_t)n * H * D, -12345.0f);
+            if (cmd == "prefill") {
+                check(g3attn_prefill(ctx, layer, start, n, Q.data(), K.data(), V.data(), gq.ptr(), gk.ptr(),
+                                     out.data()),
+                      cmd);
+            } else {
+                float *dQ = to_device(Q), *dK = to_device(K), *dV = to_device(V), *dO = to_device(out);
+                uint16_t *dq = gq.v.empty() ? nullptr : to_device(gq.v);
+                uint16_t *dk = gk.v.empty() ? nullptr : to_device(gk.v);
+                check(g3attn_prefill_device(ctx, layer, start, n, dQ, dK, dV, dq, dk, dO), cmd);
+                check(g3attn_synchronize(ctx), "g3attn_synchronize");
+                hipMemcpy(out.data(), dO, out.size() * sizeof(float), hipMemcpyDeviceToHost);
+                for (void *p : {(void *)dQ, (void *)dK, (void *)dV, (void *)dO, (void *)dq, (void *)dk}) hipFree(p);
+            }
+            write_bin(of, out.data(), out.size());
+        } else if (cmd == "decode") {
+            int layer, pos;
+            std::string qf, kf, vf, qn, kn, of;
+            in >> layer >> pos >> qf >> kf >> vf >> qn >> kn >> of;
+            if (!in || !ctx) die("bad decode line");
+            const auto q = read_bin<float>(qf, (size_t)H * D);
+            const auto k = read_bin<float>(kf, (size_t)Hkv * D);
+            const auto v = read_bin<float>(vf, (size_t)Hkv * D);
+            const Gain gq = read_gain(qn), gk = read_gain(kn);
+            std::vector<float> out((size_t)H * D, -12345.0f);
+            check(g3attn_decode(ctx, layer, pos, q.data(), k.data(), v.data(), gq.ptr(), gk.ptr(), out.data()), cmd);
+            write_bin(of, out.data(), out.size());
+        } else if (cmd == "matmul") {
+            int N, M, K;
+            std::string wf, xf, cf;
+            in >> N >> M >> K >> wf >> xf >> cf;
+            if (!in || !ctx) die("bad matmul line");
+            const auto W = read_bin<uint16_t>(wf, (size_t)M * K);
+            const auto X = read_bin<float>(xf, (size_t)N * K);
+            std::vector<float> C((size_t)N * M, -12345.0f);
+            uint16_t *dW = to_device(W);
+            float *dX = to_device(X), *dC = to_device(C);
+            check(g3attn_matmul_bf16_device(ctx, dC, dW, dX, N, M, K), cmd);
+            check(g3attn_synchronize(ctx), "g3attn_synchronize");
+            hipMemcpy(C.data(), dC, C.size() * sizeof(float), hipMemcpyDeviceToHost);
+            hipFree(dW);
+            hipFree(dX);
+            hipFree(dC);
+            write_bin(cf, C.data(), C.size());
+        } else if (cmd == "destroy") {
+            g3attn_destroy(ctx);
+            ctx = nullptr;
+        } else {
+            die("unknown command " + cmd);
+        }
+    }
+    if (ctx) g3attn_destroy(ctx);
+    hostemu_print_launches();
+    std::printf("attn_emu: ok\n");
+    return 0;
+}

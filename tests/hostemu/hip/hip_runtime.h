@@ -1,26 +1,34 @@
-// hip/hip_runtime.h for the host-emulation builds of the decode and GEMV kernels.
+// hip/hip_runtime.h for the host-emulation builds of the library's kernels.
 //
 // TEST INFRASTRUCTURE.  tests/hostemu/Makefile compiles
-// gemma3.c_amd/csrc/decode.hip and matvec.hip as plain C++ (g++,
-// -fsanitize=address,undefined)
-// with this directory first on the include path, so the kernels' own source
-// runs on the CPU under the sanitizers.  This header supplies the subset of
-// the HIP device language those kernels use, emulated on the host:
+// gemma3.c_amd/csrc/*.hip as plain C++ for x86-64 (ROCm's clang,
+// -fsanitize=address,undefined) with this directory first on the include
+// path, so the kernels' own source runs on the CPU under the sanitizers.
+// This header supplies the subset of the HIP device language those kernels
+// use, emulated on the host (the runtime API is hip_runtime_api.h):
 //
 //   - A launch runs every workgroup of the grid in turn on one team of
 //     blockDim fibers (one ucontext per GPU thread, all on the calling OS
 //     thread), so 64 consecutive fibers form one wave64.  __shared__ becomes
 //     a function-local static: one copy, used by one workgroup at a time.
 //   - __syncthreads is a barrier over the team; every cross-lane operation
-//     (DPP, v_permlane16/32_swap, __shfl_xor) is an exchange through a
-//     per-wave buffer between two barriers over the wave's 64 fibers.  A
-//     barrier or cross-lane operation that not every lane reaches leaves no
-//     fiber runnable, and the launch aborts (on the GPU it would be
-//     undefined).
-//   - Buffer loads check their offset against the descriptor's num_records
-//     and abort on an out-of-range load instead of returning zero: the
-//     kernels clamp every row index, so none may go out of range.
-//   - DPP controls other than the ones the kernels use abort.
+//     (DPP, v_permlane16/32_swap, __shfl_xor, readfirstlane, ballot, MFMA)
+//     is an exchange through a per-wave buffer between two barriers over the
+//     wave's 64 fibers.  A barrier or cross-lane operation that not every
+//     lane reaches leaves no fiber runnable, and the launch aborts (on the
+//     GPU it would be undefined).  A fiber runs until it reaches one, so the
+//     waves of a workgroup interleave at every cross-lane step.
+//   - Loads complete when issued: a buffer -> LDS fetch writes LDS at once,
+//     so one that overwrites data another wave still reads (a missing
+//     barrier) shows in the results.
+//   - Buffer loads into registers check their offset against the
+//     descriptor's num_records and abort on an out-of-range load instead of
+//     returning zero: the kernels clamp every row index, so none may go out
+//     of range.  Buffer -> LDS loads return zero there, as the hardware
+//     does: the prefill and GEMM kernels rely on it for ragged tiles.
+//   - MFMA 16x16x32 (f16 / bf16) computes the exact products and sums them
+//     in double: any operand placed in the wrong lane changes the result.
+//   - DPP controls and load forms other than the ones the kernels use abort.
 //
 // Cross-lane semantics follow AMD's CDNA4 ISA descriptions of
 // DPP quad_perm / row_mirror / row_half_mirror, V_PERMLANE16_SWAP_B32 and
@@ -62,6 +70,7 @@ struct alignas(16) uint4 { unsigned x, y, z, w; };
 inline uint4 make_uint4(unsigned x, unsigned y, unsigned z, unsigned w) { return uint4{x, y, z, w}; }
 inline float4 make_float4(float x, float y, float z, float w) { return float4{x, y, z, w}; }
 inline float2 make_float2(float x, float y) { return float2{x, y}; }
+inline uint2 make_uint2(unsigned x, unsigned y) { return uint2{x, y}; }
 
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
@@ -71,25 +80,15 @@ inline int __float_as_int(float f) { int u; std::memcpy(&u, &f, 4); return u; }
 inline float __uint_as_float(unsigned u) { float f; std::memcpy(&f, &u, 4); return f; }
 inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; }
 
-// ---- runtime API subset ------------------------------------------------------
-typedef int hipError_t;
-enum {
-    hipSuccess = 0,
-    hipErrorInvalidValue = 1,
-    hipErrorInvalidDevice = 101,
-    hipErrorInvalidSymbol = 13,
-};
-typedef void *hipStream_t;
-typedef void *hipEvent_t;
-enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 0 };
+// ---- runtime API (hip_runtime_api.h, implemented in ../hostrt.cpp) ----------
+#include "hip_runtime_api.h"
 #define HIP_SYMBOL(x) (&(x))
-
-inline hipError_t hipGetLastError() { return hipSuccess; }
-inline hipError_t hipGetDevice(int *d) { *d = 0; return hipSuccess; }
-inline hipError_t hipDeviceGetAttribute(int *v, hipDeviceAttribute_t, int) { *v = 256; return hipSuccess; }
 template <typename K>
 hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int *n, K, int, size_t) { *n = 2; return hipSuccess; }
-inline hipError_t hipGetSymbolAddress(void **p, const void *sym) { *p = const_cast<void *>(sym); return hipSuccess; }
+
+// Loads complete when issued here, so the library's explicit wait for them
+// is empty.
+#define G3K_WAIT_VMEM() ((void)0)
 
 // ---- the emulated machine ------------------------------------------------------
 // One fiber (ucontext) per thread of the workgroup, all on the calling OS
@@ -123,12 +122,14 @@ struct Barrier {
 struct Wave {
     Barrier bar;
     uint32_t a[64], b[64];
+    uint32_t op[64][8];   // MFMA A and B operands, 16 bytes each per lane
 };
 
 struct Machine {
     std::vector<Fiber> fibers;
     Barrier block;
     std::vector<Wave> waves;
+    std::vector<int> slot;   // one int per thread (__syncthreads_or)
     Fiber *current = nullptr;
     ucontext_t sched;
     void *sched_fake = nullptr;
@@ -138,7 +139,7 @@ struct Machine {
 };
 
 inline Machine *&machine() { static Machine *m = nullptr; return m; }
-inline int t_lane = 0, t_wave = 0;
+inline int t_lane = 0, t_wave = 0, t_flat = 0;
 
 // Switches from the running fiber back to the scheduler.
 inline void yield_to_scheduler(bool dying) {
@@ -181,8 +182,18 @@ inline void exchange(uint32_t x, uint32_t y, int src, uint32_t *rx, uint32_t *ry
 
 }  // namespace hostemu
 
-inline dim3 threadIdx, blockIdx;
+inline dim3 threadIdx, blockIdx, gridDim, blockDim;
 inline void __syncthreads() { hostemu::machine()->block.wait(); }
+// Barrier that also returns whether any thread of the workgroup passed nonzero.
+inline int __syncthreads_or(int p) {
+    hostemu::Machine &m = *hostemu::machine();
+    m.slot[hostemu::t_flat] = p != 0;
+    m.block.wait();
+    int r = 0;
+    for (int v : m.slot) r |= v;
+    m.block.wait();   // every thread has read the slots before any rewrites them
+    return r;
+}
 
 // ---- cross-lane builtins ---------------------------------------------------------
 // DPP (row = 16 lanes): quad_perm 0x00-0xff, row_ror:8 0x128 (lane i reads
@@ -274,6 +285,89 @@ inline std::array<uint32_t, 4> hostemu_raw_buffer_load_b128(__amdgpu_buffer_rsrc
 #define __builtin_amdgcn_make_buffer_rsrc hostemu_make_buffer_rsrc
 #define __builtin_amdgcn_raw_buffer_load_b128 hostemu_raw_buffer_load_b128
 
+// Buffer -> LDS load (gfx950 buffer_load_dwordx4 ... lds), 16 bytes per lane:
+// lane l's 16 bytes go to LDS at the given base + 16 l.  A dword whose
+// offset + 4 exceeds num_records reads zero, as the hardware's range check
+// for a raw (stride 0) buffer gives; the kernels rely on this for ragged
+// tiles.  Other sizes and a nonzero instruction offset abort.
+template <typename P>
+inline void hostemu_buffer_load_lds(__amdgpu_buffer_rsrc_t r, P lds, int size, unsigned voff, unsigned soff,
+                                    int offset, int aux) {
+    (void)aux;
+    if (size != 16 || offset != 0) hostemu::fail("buffer->LDS load form not emulated");
+    char *dst = (char *)lds + 16 * hostemu::t_lane;
+    for (int i = 0; i < 4; i++) {
+        const uint64_t o = (uint64_t)voff + soff + 4 * i;
+        uint32_t v = 0;
+        if (o + 4 <= r.num_records) std::memcpy(&v, r.base + o, 4);
+        std::memcpy(dst + 4 * i, &v, 4);
+    }
+}
+#define __builtin_amdgcn_raw_ptr_buffer_load_lds hostemu_buffer_load_lds
+
+// ---- wave-level builtins ------------------------------------------------------------
+inline int hostemu_readfirstlane(int v) {
+    uint32_t r, unused;
+    hostemu::exchange((uint32_t)v, 0, 0, &r, &unused);
+    return (int)r;
+}
+#define __builtin_amdgcn_readfirstlane hostemu_readfirstlane
+
+inline uint64_t hostemu_ballot_w64(bool p) {
+    hostemu::Wave &w = hostemu::machine()->waves[hostemu::t_wave];
+    w.a[hostemu::t_lane] = p;
+    w.bar.wait();
+    uint64_t mask = 0;
+    for (int i = 0; i < 64; i++) mask |= (uint64_t)(w.a[i] != 0) << i;
+    w.bar.wait();
+    return mask;
+}
+#define __builtin_amdgcn_ballot_w64 hostemu_ballot_w64
+
+// Scheduling hints have no effect here.
+#define __builtin_amdgcn_s_setprio(x) ((void)(x))
+#define __builtin_amdgcn_sched_barrier(x) ((void)(x))
+
+// V_MFMA_F32_16X16X32_{F16,BF16}: D = A B + C for a 16 x 32 A, a 32 x 16 B
+// and 16 x 16 C / D, one wave.  Operand layout (the one the kernels are
+// written to): lane l holds A[l % 16][8 (l / 16) + j] and
+// B[8 (l / 16) + j][l % 16] as element j of its 8-element operands, and
+// D[4 (l / 16) + r][l % 16] as element r of its 4 accumulators.  The
+// products are summed in double and rounded once (the hardware's fp32
+// summation order is not modelled).  Broadcast controls abort.
+template <typename V8, typename F4>
+inline F4 hostemu_mfma_16x16x32(V8 a, V8 b, F4 c, int cbsz, int abid, int blgp) {
+    static_assert(sizeof(V8) == 16, "8 x 16-bit operands");
+    if (cbsz || abid || blgp) hostemu::fail("MFMA broadcast controls not emulated");
+    hostemu::Wave &w = hostemu::machine()->waves[hostemu::t_wave];
+    const int l = hostemu::t_lane;
+    std::memcpy(&w.op[l][0], &a, 16);
+    std::memcpy(&w.op[l][4], &b, 16);
+    w.bar.wait();
+    const int n = l & 15, g = l >> 4;
+    float bcol[32];
+    for (int q = 0; q < 4; q++) {
+        V8 bv;
+        std::memcpy(&bv, &w.op[n + 16 * q][4], 16);
+        for (int j = 0; j < 8; j++) bcol[8 * q + j] = (float)bv[j];
+    }
+    F4 d;
+    for (int r = 0; r < 4; r++) {
+        const int m = 4 * g + r;
+        double acc = (double)c[r];
+        for (int q = 0; q < 4; q++) {
+            V8 av;
+            std::memcpy(&av, &w.op[m + 16 * q][0], 16);
+            for (int j = 0; j < 8; j++) acc += (double)(float)av[j] * (double)bcol[8 * q + j];
+        }
+        d[r] = (float)acc;
+    }
+    w.bar.wait();
+    return d;
+}
+#define __builtin_amdgcn_mfma_f32_16x16x32_f16 hostemu_mfma_16x16x32
+#define __builtin_amdgcn_mfma_f32_16x16x32_bf16 hostemu_mfma_16x16x32
+
 // ---- launches ------------------------------------------------------------------------
 namespace hostemu {
 
@@ -288,6 +382,8 @@ inline void fiber_entry() {
     fail("finished fiber resumed");
 }
 
+inline unsigned workgroups(dim3 g) { return g.x * g.y * g.z; }
+
 // Runs every workgroup of `grid` in order on one team of blockDim fibers.
 template <typename K, typename... A>
 void launch(K kernel, dim3 grid, dim3 block, A... args) {
@@ -295,9 +391,12 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
     if (nt % 64) fail("workgroup size not a multiple of 64");
     Machine m;
     machine() = &m;
+    gridDim = grid;
+    blockDim = block;
     m.fibers = std::vector<Fiber>(nt);
     m.block.n = nt;
     m.waves = std::vector<Wave>(nt / 64);
+    m.slot = std::vector<int>(nt);
     for (auto &w : m.waves) w.bar.n = 64;
     m.body = [&] {
         for (unsigned z = 0; z < grid.z; z++)
@@ -331,6 +430,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
             threadIdx = f.tid;
             t_lane = f.lane;
             t_wave = f.wave;
+            t_flat = (int)(&f - m.fibers.data());
 #if defined(__SANITIZE_ADDRESS__)
             __sanitizer_start_switch_fiber(&m.sched_fake, f.stack, f.stack_size);
 #endif
@@ -349,6 +449,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 }  // namespace hostemu
 
 #define hipLaunchKernelGGL(kernel, grid, block, shmem, stream, ...) \
-    hostemu::launch(kernel, dim3(grid), dim3(block), __VA_ARGS__)
+    ((void)(stream), hostemu_count_launch(#kernel, hostemu::workgroups(dim3(grid))), \
+     hostemu::launch(kernel, dim3(grid), dim3(block), __VA_ARGS__))
 
 #endif

@@ -1,0 +1,250 @@
+"""The whole library (gemma3.c_amd/host + every kernel) behind its C ABI, run
+on the CPU under ASan + UBSan on the emulated wave64 machine of tests/hostemu.
+
+tests/hostemu/_build/attn_emu executes a script of g3attn calls (create,
+kv_write, prefill, decode, kv_read, matmul) against the library compiled for
+the host: the host code's staging ranges, key-split choice, ring handling
+and buffer sizing run unchanged, and the kernels run from their own source
+with MFMA, DPP, permlane swaps and buffer -> LDS loads emulated (see
+hostemu/hip/hip_runtime.h).  Each call sequence is mirrored on the oracle,
+whose caches carry state from call to call exactly as the library's do:
+prefill chunks, the history they stage from the cache, the sliding-window
+ring, decode steps after a prefill.
+
+Expected values: the oracle's g3o_prefill / g3o_layer_decode (restating
+gemma3_transformer.c:641-692 and :294-352; the bar is the path's 2e-3 x
+output RMS, and the emulated kernels land near 1e-5, as on the GPU), the
+cache rows the reference's cache_kv leaves (gemma3_transformer.c:236-251),
+and an fp64 product for the batched-prefill GEMM.  What this adds to the GPU
+tests: no out-of-range access or undefined behaviour in the host code or
+the kernels' indexing (LDS rings, ragged tiles, key splits) under the
+sanitizers; a barrier or cross-lane operation that some lane misses stops
+the run.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from helpers import O, REPO, TOL, rel_err
+
+EMU = os.path.join(REPO, "tests", "hostemu")
+EXE = os.path.join(EMU, "_build", "attn_emu")
+D = 256
+CLANG = "/opt/rocm/lib/llvm/bin/clang++"
+
+pytestmark = pytest.mark.skipif(not os.path.exists(CLANG), reason="ROCm clang not available")
+
+
+@pytest.fixture(scope="module")
+def built():
+    r = subprocess.run(["make", "-C", EMU, "-j8"], capture_output=True, text=True, timeout=900)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    return True
+
+
+def _bf16_valued(a):
+    """Round to the nearest bf16 value (the configs' inputs are bf16-valued)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).view(np.float32)
+
+
+class Emu:
+    """A script of library calls and the same calls on the oracle."""
+
+    def __init__(self, tmp, H=8, Hkv=4, max_context=128, window=16, layers=6):
+        self.dir, self.H, self.Hkv = str(tmp), H, Hkv
+        self.cfg = O.Config(max_context=max_context, sliding_window=window, num_heads=H, num_kv_heads=Hkv)
+        self.tables = {False: O.rope_table(max_context, 10000.0), True: O.rope_table(max_context, 1e6)}
+        self._save("rl.bin", self.tables[False])
+        self._save("rg.bin", self.tables[True])
+        self.lines = [f"create {H} {Hkv} {max_context} {window} {layers} 1e-6 rl.bin rg.bin"]
+        self.caches = {}
+        self.checks = []          # (file, expected, label, bar: x RMS, 0 = exact, or an array bound)
+        self.k = 0
+        self.rng = np.random.default_rng(1234)
+
+    def _save(self, name, a):
+        np.ascontiguousarray(a).tofile(os.path.join(self.dir, name))
+
+    def _name(self, stem):
+        self.k += 1
+        return f"{stem}{self.k}.bin"
+
+    def _cache(self, layer):
+        if layer not in self.caches:
+            rows = self.cfg.cache_rows(layer)
+            self.caches[layer] = (np.zeros((rows, self.Hkv * D), np.float32),
+                                  np.zeros((rows, self.Hkv * D), np.float32))
+        return self.caches[layer]
+
+    def inputs(self, n, bf16=True):
+        f = _bf16_valued if bf16 else (lambda a: a.astype(np.float32))
+        return (f(self.rng.standard_normal((n, self.H * D))), f(self.rng.standard_normal((n, self.Hkv * D))),
+                f(self.rng.standard_normal((n, self.Hkv * D))))
+
+    def gains(self, norm):
+        """None (no QK-norm), or non-unit bf16 gains for q and k."""
+        if not norm:
+            return None, None, "-", "-"
+        g = [(_bf16_valued(self.rng.standard_normal(D) * 0.3).view(np.uint32) >> 16).astype(np.uint16)
+             for _ in range(2)]
+        names = [self._name("gq"), self._name("gk")]
+        self._save(names[0], g[0])
+        self._save(names[1], g[1])
+        return g[0], g[1], names[0], names[1]
+
+    def prefill(self, layer, start, n, norm=True, bf16=True, device=False):
+        Q, K, V = self.inputs(n, bf16)
+        gq, gk, nq, nk = self.gains(norm)
+        files = [self._name(s) for s in ("Q", "K", "V", "out")]
+        for f, a in zip(files, (Q, K, V)):
+            self._save(f, a)
+        cmd = "prefill_device" if device else "prefill"
+        self.lines.append(f"{cmd} {layer} {start} {n} {files[0]} {files[1]} {files[2]} {nq} {nk} {files[3]}")
+        Kc, Vc = self._cache(layer)
+        want, _, _ = O.prefill(self.cfg, layer, start, Q, K, V, Kc, Vc,
+                               self.tables[O.is_global_layer(layer)], gq, gk)
+        self.checks.append((files[3], want, f"prefill layer={layer} start={start} n={n}", TOL))
+
+    def decode(self, layer, pos, norm=True):
+        Q, K, V = self.inputs(1)
+        gq, gk, nq, nk = self.gains(norm)
+        files = [self._name(s) for s in ("q", "k", "v", "o")]
+        for f, a in zip(files, (Q, K, V)):
+            self._save(f, a)
+        self.lines.append(f"decode {layer} {pos} {files[0]} {files[1]} {files[2]} {nq} {nk} {files[3]}")
+        Kc, Vc = self._cache(layer)
+        want, _, _ = O.layer_decode(self.cfg, layer, pos, Q[0], K[0], V[0], Kc, Vc,
+                                    self.tables[O.is_global_layer(layer)], gq, gk)
+        self.checks.append((files[3], want, f"decode layer={layer} pos={pos}", TOL))
+
+    def check_cache(self, layer, slot, n):
+        """The cache rows [slot, slot + n) as the oracle's cache_kv left them."""
+        kf, vf = self._name("kr"), self._name("vr")
+        self.lines.append(f"kv_read {layer} {slot} {n} {kf} {vf}")
+        Kc, Vc = self._cache(layer)
+        self.checks.append((kf, Kc[slot:slot + n].copy(), f"cache k layer={layer} [{slot},{slot + n})", 1e-5))
+        self.checks.append((vf, Vc[slot:slot + n].copy(), f"cache v layer={layer} [{slot},{slot + n})", 0.0))
+
+    def matmul(self, N, M, K):
+        W = (_bf16_valued(self.rng.standard_normal((M, K)) * 0.05).view(np.uint32) >> 16).astype(np.uint16)
+        X = self.rng.standard_normal((N, K)).astype(np.float32)
+        files = [self._name(s) for s in ("W", "X", "C")]
+        self._save(files[0], W)
+        self._save(files[1], X)
+        self.lines.append(f"matmul {N} {M} {K} {files[0]} {files[1]} {files[2]}")
+        W64 = (W.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        X64 = X.astype(np.float64)
+        # elementwise: the hi / lo split of X (2^-17 relative each) and fp32
+        # accumulation over K terms
+        bound = (2.0 ** -16 + K * 2.0 ** -24) * (np.abs(X64) @ np.abs(W64).T) + 1e-30
+        self.checks.append((files[2], X64 @ W64.T, f"matmul N={N} M={M} K={K} (max err / bound)", bound))
+
+    def run(self, **env):
+        with open(os.path.join(self.dir, "script.txt"), "w") as f:
+            f.write("\n".join(self.lines) + "\n")
+        e = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="print_stacktrace=1")
+        e.update({k: str(v) for k, v in env.items()})
+        res = subprocess.run([EXE, self.dir], capture_output=True, text=True, timeout=1200, env=e)
+        assert res.returncode == 0 and "attn_emu: ok" in res.stdout, res.stdout[-2000:] + res.stderr[-4000:]
+        assert "runtime error" not in res.stderr and "AddressSanitizer" not in res.stderr, res.stderr[-4000:]
+        for f, want, label, bar in self.checks:
+            got = np.fromfile(os.path.join(self.dir, f), dtype=np.float32).reshape(np.shape(want))
+            if isinstance(bar, np.ndarray):
+                err, bar = float(np.max(np.abs(got - want) / bar)), 1.0
+            else:
+                err = rel_err(got, want) if bar else float(np.abs(got - want).max())
+            print(f"[hostemu attn] {label}: {err:.3e}")
+            assert err <= bar, (label, err)
+        # "launch <kernel expression> <launches> <workgroups>": workgroups
+        # summed over launches, keyed by the bare kernel name
+        launches = {}
+        for ln in res.stdout.splitlines():
+            if ln.startswith("launch "):
+                expr, count, wgs = ln[len("launch "):].rsplit(" ", 2)
+                name = expr.strip("()").split("<")[0]
+                c, w = launches.get(name, (0, 0))
+                launches[name] = (c + int(count), w + int(wgs))
+        return launches
+
+
+def test_global_prefill_chunks_then_decode(built, tmp_path):
+    """Global layer: a ragged first chunk, a second chunk that stages its
+    history from the cache, then two decode steps on the cache it wrote."""
+    e = Emu(tmp_path)
+    e.prefill(5, 0, 40)
+    e.prefill(5, 40, 30)
+    e.decode(5, 70)
+    e.decode(5, 71)
+    e.check_cache(5, 0, 72)
+    launches = e.run()
+    assert launches["stage_kernel"][0] == 3   # the batch's values x 2, the history once
+
+
+def test_local_prefill_ring(built, tmp_path):
+    """Local layer, window 16: a 40-token batch (longer than the ring: only
+    its last 16 rows are cached), a chunk whose history wraps the ring, and
+    a decode step."""
+    e = Emu(tmp_path)
+    e.prefill(0, 0, 40)
+    e.prefill(0, 40, 21)
+    e.decode(0, 61)
+    e.check_cache(0, 0, 16)
+    e.run()
+
+
+def test_key_splits(built, tmp_path):
+    """Global prefills long enough for the host's makespan model to split the
+    key tiles of every 64-query block over 2 (n = 256: 4 blocks) and 4
+    (n = 512: 8 blocks) workgroups, with the merge launch (one KV head)."""
+    for n, splits in [(256, 2), (512, 4)]:
+        d = tmp_path / str(n)
+        d.mkdir()
+        e = Emu(d, H=2, Hkv=1, max_context=640, window=64)
+        e.prefill(5, 0, n)
+        launches = e.run()
+        assert launches["prefill_kernel"] == (1, n // 64 * splits), launches
+        assert launches["prefill_combine_kernel"][0] == 1, launches
+
+
+def test_fp32_values_take_the_v_lo_pass(built, tmp_path):
+    """Inputs that are not bf16-valued: the staging kernel flags V_lo and the
+    kernel adds the P_hi.V_lo pass; also with QK-norm absent."""
+    e = Emu(tmp_path)
+    e.prefill(5, 0, 70, bf16=False)
+    e.prefill(0, 0, 24, bf16=False, norm=False)
+    e.run()
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (8, 2)])
+def test_gqa_groups(built, tmp_path, heads, kv_heads):
+    """GQA groups 1 and 4 (the configs use 2), prefill and decode."""
+    e = Emu(tmp_path, H=heads, Hkv=kv_heads)
+    e.prefill(5, 0, 50)
+    e.decode(5, 50)
+    e.prefill(0, 0, 20)
+    e.run()
+
+
+@pytest.mark.parametrize("env", [{"G3ATTN_PREFILL_QPW": 32}, {"G3ATTN_PREFILL_SCHED": 0},
+                                 {"G3ATTN_PREFILL_SCHED": 2}])
+def test_prefill_variants(built, tmp_path, env):
+    """The selectable prefill forms: 32 queries per wave, and the two other
+    SIMD phase schedules."""
+    e = Emu(tmp_path)
+    e.prefill(5, 0, 70)
+    e.prefill(0, 0, 33)
+    e.run(**env)
+
+
+def test_device_entry_and_matmul(built, tmp_path):
+    """g3attn_prefill_device, and the batched-prefill GEMM at ragged N with
+    its one-plane (M = 4 multiple) and K = 96 shapes against fp64."""
+    e = Emu(tmp_path)
+    e.prefill(5, 0, 20, device=True)
+    e.matmul(40, 64, 96)
+    e.matmul(130, 20, 64)
+    launches = e.run()
+    assert launches["gemm_kernel"][0] == 2, launches

@@ -22,7 +22,6 @@ on and off, non-temporal and plain loads, groups 1 / 2 / 4, and the
 gemma3_gqa-shaped path with and without an additive mask.
 """
 import os
-import shutil
 import subprocess
 
 import numpy as np
@@ -35,7 +34,8 @@ BUILD = os.path.join(EMU, "_build")
 LOG2E = 1.4426950408889634
 BAR = 1e-4  # max-abs error / output RMS, the fp32 decode bar
 
-pytestmark = pytest.mark.skipif(not shutil.which("g++"), reason="g++ not available")
+pytestmark = pytest.mark.skipif(not os.path.exists("/opt/rocm/lib/llvm/bin/clang++"),
+                                reason="ROCm clang not available")
 
 
 @pytest.fixture(scope="module")

@@ -17,7 +17,6 @@ out-of-range access or undefined behaviour in the kernel's indexing, ragged
 tails and prologue, under the sanitizers.
 """
 import os
-import shutil
 import subprocess
 
 import numpy as np
@@ -30,7 +29,8 @@ EXE = os.path.join(EMU, "_build", "matvec_emu")
 BAR = 1e-5
 GEGLU = 1
 
-pytestmark = pytest.mark.skipif(not shutil.which("g++"), reason="g++ not available")
+pytestmark = pytest.mark.skipif(not os.path.exists("/opt/rocm/lib/llvm/bin/clang++"),
+                                reason="ROCm clang not available")
 
 
 @pytest.fixture(scope="module")

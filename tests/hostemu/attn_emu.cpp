@@ -10,16 +10,24 @@
 // return stops the run with exit status 1 and the library's error text.
 //
 //   create H Hkv max_context window num_layers eps rope_local rope_global
+//          [hidden intermediate vocab]
 //   kv_write layer slot n k v                  (rows [n][Hkv][256])
 //   kv_read layer slot n k_out v_out
 //   prefill layer start_pos n Q K V q_norm k_norm out
 //   prefill_device ...                          (same, device pointers)
 //   decode layer pos q k v q_norm k_norm out
 //   matmul N M K W X C                          (g3attn_matmul_bf16_device)
+//   model prefix     the model's bf16 tensors from prefix + "embed.bin",
+//                    "norm.bin" and "L<l>_<tensor>.bin" (a missing file is a
+//                    NULL tensor), kept in host memory and as device copies
+//   upload                                      (g3attn_upload_weights, host)
+//   forward_device token pos logits|-           (the device copies)
+//   forward_token token pos logits              (the uploaded model)
+//   prefill_tokens n tokens start logits        (the uploaded model)
 //   destroy
 //
-// At the end it prints "launch <kernel> <count>" for every kernel launched
-// and "attn_emu: ok".
+// At the end it prints "launch <kernel> <launches> <workgroups> <ms>" for every
+// kernel launched and "attn_emu: ok".
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -33,6 +41,11 @@
 #include "g3attn.h"
 
 namespace {
+
+const char *const kLayerTensors[13] = {
+    "input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
+    "post_attention_layernorm", "gate_proj", "up_proj", "down_proj", "pre_feedforward_layernorm",
+    "post_feedforward_layernorm"};
 
 std::string g_dir;
 
@@ -77,6 +90,45 @@ T *to_device(const std::vector<T> &h) {
     return static_cast<T *>(d);
 }
 
+bool exists(const std::string &name) {
+    FILE *f = std::fopen((g_dir + "/" + name).c_str(), "rb");
+    if (f) std::fclose(f);
+    return f != nullptr;
+}
+
+size_t file_elems(const std::string &name, size_t elem) {
+    FILE *f = std::fopen((g_dir + "/" + name).c_str(), "rb");
+    if (!f) die("cannot open " + name);
+    std::fseek(f, 0, SEEK_END);
+    const long n = std::ftell(f);
+    std::fclose(f);
+    return (size_t)n / elem;
+}
+
+// A model's tensors: host arrays (for g3attn_upload_weights) and device
+// copies (for g3attn_forward_device), in g3attn_weights structs.
+struct Model {
+    std::vector<std::vector<uint16_t>> host;
+    std::vector<void *> dev;
+    g3attn_weights h{}, d{};
+    const uint16_t *load(const std::string &name, const uint16_t **dev_slot) {
+        if (!exists(name)) {
+            *dev_slot = nullptr;
+            return nullptr;
+        }
+        host.push_back(read_bin<uint16_t>(name, file_elems(name, 2)));
+        void *p = nullptr;
+        if (hipMalloc(&p, host.back().size() * 2) != hipSuccess) die("hipMalloc");
+        hipMemcpy(p, host.back().data(), host.back().size() * 2, hipMemcpyHostToDevice);
+        dev.push_back(p);
+        *dev_slot = static_cast<const uint16_t *>(p);
+        return host.back().data();
+    }
+    ~Model() {
+        for (void *p : dev) hipFree(p);
+    }
+};
+
 void check(int rc, const std::string &call) {
     if (rc) {
         std::fprintf(stderr, "attn_emu: %s returned %d: %s\n", call.c_str(), rc, g3attn_last_error());
@@ -92,7 +144,8 @@ int main(int argc, char **argv) {
     std::ifstream script(g_dir + "/script.txt");
     if (!script) die("no script.txt");
     g3attn_ctx *ctx = nullptr;
-    int H = 0, Hkv = 0;
+    int H = 0, Hkv = 0, layers = 0, hidden = 0, vocab = 0;
+    Model *model = nullptr;
     const size_t D = 256;
     std::string line;
     while (std::getline(script, line)) {
@@ -100,11 +153,12 @@ int main(int argc, char **argv) {
         std::string cmd;
         if (!(in >> cmd) || cmd[0] == '#') continue;
         if (cmd == "create") {
-            int max_ctx, window, layers;
+            int max_ctx, window, inter = 0;
             float eps;
             std::string rl, rg;
             in >> H >> Hkv >> max_ctx >> window >> layers >> eps >> rl >> rg;
             if (!in) die("bad create line");
+            if (!(in >> hidden >> inter >> vocab)) hidden = inter = vocab = 0;
             g3attn_config cfg;
             g3attn_default_config(&cfg);
             cfg.num_heads = H;
@@ -113,6 +167,11 @@ int main(int argc, char **argv) {
             cfg.sliding_window = window;
             cfg.num_layers = layers;
             cfg.rmsnorm_eps = eps;
+            if (hidden) {
+                cfg.hidden_size = hidden;
+                cfg.intermediate_size = inter;
+                cfg.vocab_size = vocab;
+            }
             const auto tl = read_bin<float>(rl, (size_t)max_ctx * D);
             const auto tg = read_bin<float>(rg, (size_t)max_ctx * D);
             ctx = g3attn_create(&cfg, max_ctx, tl.data(), tg.data());
@@ -188,6 +247,47 @@ int main(int argc, char **argv) {
             hipFree(dX);
             hipFree(dC);
             write_bin(cf, C.data(), C.size());
+        } else if (cmd == "model") {
+            std::string prefix;
+            in >> prefix;
+            if (!in || model) die("bad model line");
+            model = new Model;
+            model->h.embed_tokens = model->load(prefix + "embed.bin", &model->d.embed_tokens);
+            model->h.norm = model->load(prefix + "norm.bin", &model->d.norm);
+            for (int l = 0; l < layers; l++) {
+                const uint16_t **hs = reinterpret_cast<const uint16_t **>(&model->h.layers[l]);
+                const uint16_t **ds = reinterpret_cast<const uint16_t **>(&model->d.layers[l]);
+                for (int t = 0; t < 13; t++)
+                    hs[t] = model->load(prefix + "L" + std::to_string(l) + "_" + kLayerTensors[t] + ".bin", &ds[t]);
+            }
+        } else if (cmd == "upload") {
+            if (!ctx || !model) die("upload needs a context and a model");
+            check(g3attn_upload_weights(ctx, &model->h), cmd);
+        } else if (cmd == "forward_device" || cmd == "forward_token") {
+            int token, pos;
+            std::string lf;
+            in >> token >> pos >> lf;
+            if (!in || !ctx || !model) die("bad " + cmd + " line");
+            std::vector<float> logits((size_t)vocab, -12345.0f);
+            if (cmd == "forward_token") {
+                check(g3attn_forward_token(ctx, token, pos, logits.data(), 1), cmd);
+            } else {
+                float *dl = lf == "-" ? nullptr : to_device(logits);
+                check(g3attn_forward_device(ctx, &model->d, token, pos, dl, dl != nullptr, nullptr), cmd);
+                check(g3attn_synchronize(ctx), "g3attn_synchronize");
+                if (dl) hipMemcpy(logits.data(), dl, logits.size() * sizeof(float), hipMemcpyDeviceToHost);
+                hipFree(dl);
+            }
+            if (lf != "-") write_bin(lf, logits.data(), logits.size());
+        } else if (cmd == "prefill_tokens") {
+            int n, start;
+            std::string tf, lf;
+            in >> n >> tf >> start >> lf;
+            if (!in || !ctx || !model) die("bad prefill_tokens line");
+            const auto tokens = read_bin<int>(tf, (size_t)n);
+            std::vector<float> logits((size_t)vocab, -12345.0f);
+            check(g3attn_prefill_tokens(ctx, tokens.data(), n, start, logits.data()), cmd);
+            write_bin(lf, logits.data(), logits.size());
         } else if (cmd == "destroy") {
             g3attn_destroy(ctx);
             ctx = nullptr;
@@ -196,6 +296,7 @@ int main(int argc, char **argv) {
         }
     }
     if (ctx) g3attn_destroy(ctx);
+    delete model;
     hostemu_print_launches();
     std::printf("attn_emu: ok\n");
     return 0;

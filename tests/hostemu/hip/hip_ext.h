@@ -10,8 +10,7 @@
     do {                                                                                    \
         hipEvent_t hostemu_e0 = (ev0), hostemu_e1 = (ev1);                                  \
         if (hostemu_e0) hipEventRecord(hostemu_e0, (stream));                                \
-        hostemu_count_launch(#kernel, hostemu::workgroups(dim3(grid)));                     \
-        hostemu::launch(kernel, dim3(grid), dim3(block), __VA_ARGS__);                      \
+        hostemu::launch_named(#kernel, kernel, dim3(grid), dim3(block), __VA_ARGS__);       \
         if (hostemu_e1) hipEventRecord(hostemu_e1, (stream));                                \
     } while (0)
 

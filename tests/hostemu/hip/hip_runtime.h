@@ -8,13 +8,13 @@
 // use, emulated on the host (the runtime API is hip_runtime_api.h):
 //
 //   - A launch runs every workgroup of the grid in turn on one team of
-//     blockDim fibers (one ucontext per GPU thread, all on the calling OS
+//     blockDim fibers (one stack per GPU thread, all on the calling OS
 //     thread), so 64 consecutive fibers form one wave64.  __shared__ becomes
 //     a function-local static: one copy, used by one workgroup at a time.
 //   - __syncthreads is a barrier over the team; every cross-lane operation
 //     (DPP, v_permlane16/32_swap, __shfl_xor, readfirstlane, ballot, MFMA)
-//     is an exchange through a per-wave buffer between two barriers over the
-//     wave's 64 fibers.  A barrier or cross-lane operation that not every
+//     is an exchange through a double-buffered per-wave buffer with one
+//     barrier over the wave's 64 fibers.  A barrier or cross-lane operation that not every
 //     lane reaches leaves no fiber runnable, and the launch aborts (on the
 //     GPU it would be undefined).  A fiber runs until it reaches one, so the
 //     waves of a workgroup interleave at every cross-lane step.
@@ -43,7 +43,6 @@
 #include <cstring>
 #include <math.h>
 #include <functional>
-#include <ucontext.h>
 #include <vector>
 #if defined(__SANITIZE_ADDRESS__)
 #include <sanitizer/common_interface_defs.h>
@@ -91,9 +90,18 @@ hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int *n, K, int, size_t) 
 #define G3K_WAIT_VMEM() ((void)0)
 
 // ---- the emulated machine ------------------------------------------------------
-// One fiber (ucontext) per thread of the workgroup, all on the calling OS
-// thread: a barrier parks the fiber and the scheduler resumes the next
-// runnable one in order.  Deterministic, and no OS-thread contention.
+// One fiber per thread of the workgroup, all on the calling OS thread: a
+// barrier parks the fiber and the scheduler resumes the next runnable one in
+// order.  Deterministic, and no OS-thread contention.
+//
+// hostemu_switch(from, to) is the x86-64 SysV stack switch: it pushes the
+// callee-saved registers and the SSE / x87 control words, stores the stack
+// pointer in *from, loads `to` and pops the same from there.  (glibc's
+// swapcontext also saves the signal mask with a system call each time.)
+// Defined in ../hostrt.cpp.
+extern "C" void hostemu_switch(void **from, void *to);
+
+
 namespace hostemu {
 
 [[noreturn]] inline void fail(const char *what) {
@@ -103,7 +111,7 @@ namespace hostemu {
 }
 
 struct Fiber {
-    ucontext_t ctx;
+    void *sp = nullptr;       // saved stack pointer while switched out
     char *stack = nullptr;
     size_t stack_size = 0;
     void *fake_stack = nullptr;
@@ -119,10 +127,15 @@ struct Barrier {
     void wait();
 };
 
+// Per-wave exchange buffers, two of each: exchange k of a wave uses set
+// k % 2, so one barrier per exchange suffices.  A lane can write set k % 2
+// again only at exchange k + 2, after passing exchange k + 1's barrier, which
+// every lane reaches only after reading exchange k.
 struct Wave {
     Barrier bar;
-    uint32_t a[64], b[64];
-    uint32_t op[64][8];   // MFMA A and B operands, 16 bytes each per lane
+    uint32_t a[2][64], b[2][64];
+    uint32_t op[2][64][8];   // MFMA A and B operands, 16 bytes each per lane
+    unsigned gen[64] = {};   // exchanges each lane has started
 };
 
 struct Machine {
@@ -131,7 +144,7 @@ struct Machine {
     std::vector<Wave> waves;
     std::vector<int> slot;   // one int per thread (__syncthreads_or)
     Fiber *current = nullptr;
-    ucontext_t sched;
+    void *sched_sp = nullptr;
     void *sched_fake = nullptr;
     const void *sched_bottom = nullptr;
     size_t sched_size = 0;
@@ -150,7 +163,7 @@ inline void yield_to_scheduler(bool dying) {
 #else
     (void)dying;
 #endif
-    swapcontext(&f->ctx, &m.sched);
+    hostemu_switch(&f->sp, m.sched_sp);
 #if defined(__SANITIZE_ADDRESS__)
     __sanitizer_finish_switch_fiber(f->fake_stack, nullptr, nullptr);
 #endif
@@ -171,13 +184,13 @@ inline void Barrier::wait() {
 // Every lane publishes (x, y); each returns the pair published by lane src.
 inline void exchange(uint32_t x, uint32_t y, int src, uint32_t *rx, uint32_t *ry) {
     Wave &w = machine()->waves[t_wave];
-    w.a[t_lane] = x;
-    w.b[t_lane] = y;
+    const int k = w.gen[t_lane]++ & 1;
+    w.a[k][t_lane] = x;
+    w.b[k][t_lane] = y;
     w.bar.wait();
     if (src < 0 || src >= 64) fail("cross-lane source lane out of range");
-    *rx = w.a[src];
-    *ry = w.b[src];
-    w.bar.wait();
+    *rx = w.a[k][src];
+    *ry = w.b[k][src];
 }
 
 }  // namespace hostemu
@@ -315,11 +328,11 @@ inline int hostemu_readfirstlane(int v) {
 
 inline uint64_t hostemu_ballot_w64(bool p) {
     hostemu::Wave &w = hostemu::machine()->waves[hostemu::t_wave];
-    w.a[hostemu::t_lane] = p;
+    const int k = w.gen[hostemu::t_lane]++ & 1;
+    w.a[k][hostemu::t_lane] = p;
     w.bar.wait();
     uint64_t mask = 0;
-    for (int i = 0; i < 64; i++) mask |= (uint64_t)(w.a[i] != 0) << i;
-    w.bar.wait();
+    for (int i = 0; i < 64; i++) mask |= (uint64_t)(w.a[k][i] != 0) << i;
     return mask;
 }
 #define __builtin_amdgcn_ballot_w64 hostemu_ballot_w64
@@ -341,14 +354,15 @@ inline F4 hostemu_mfma_16x16x32(V8 a, V8 b, F4 c, int cbsz, int abid, int blgp) 
     if (cbsz || abid || blgp) hostemu::fail("MFMA broadcast controls not emulated");
     hostemu::Wave &w = hostemu::machine()->waves[hostemu::t_wave];
     const int l = hostemu::t_lane;
-    std::memcpy(&w.op[l][0], &a, 16);
-    std::memcpy(&w.op[l][4], &b, 16);
+    const int k = w.gen[l]++ & 1;
+    std::memcpy(&w.op[k][l][0], &a, 16);
+    std::memcpy(&w.op[k][l][4], &b, 16);
     w.bar.wait();
     const int n = l & 15, g = l >> 4;
     float bcol[32];
     for (int q = 0; q < 4; q++) {
         V8 bv;
-        std::memcpy(&bv, &w.op[n + 16 * q][4], 16);
+        std::memcpy(&bv, &w.op[k][n + 16 * q][4], 16);
         for (int j = 0; j < 8; j++) bcol[8 * q + j] = (float)bv[j];
     }
     F4 d;
@@ -357,12 +371,11 @@ inline F4 hostemu_mfma_16x16x32(V8 a, V8 b, F4 c, int cbsz, int abid, int blgp) 
         double acc = (double)c[r];
         for (int q = 0; q < 4; q++) {
             V8 av;
-            std::memcpy(&av, &w.op[m + 16 * q][0], 16);
+            std::memcpy(&av, &w.op[k][m + 16 * q][0], 16);
             for (int j = 0; j < 8; j++) acc += (double)(float)av[j] * (double)bcol[8 * q + j];
         }
         d[r] = (float)acc;
     }
-    w.bar.wait();
     return d;
 }
 #define __builtin_amdgcn_mfma_f32_16x16x32_f16 hostemu_mfma_16x16x32
@@ -383,6 +396,18 @@ inline void fiber_entry() {
 }
 
 inline unsigned workgroups(dim3 g) { return g.x * g.y * g.z; }
+
+// Fiber stacks, allocated once per thread index and reused by every launch.
+// The pool is never destroyed, so the stacks stay reachable at exit (no
+// leak report).
+inline char *stack_pool(int i, size_t bytes) {
+    static std::vector<char *> *pool = new std::vector<char *>;
+    while ((int)pool->size() <= i) {
+        pool->push_back(static_cast<char *>(std::malloc(bytes)));
+        if (!pool->back()) fail("fiber stack allocation");
+    }
+    return (*pool)[i];
+}
 
 // Runs every workgroup of `grid` in order on one team of blockDim fibers.
 template <typename K, typename... A>
@@ -413,13 +438,20 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
         f.tid = dim3(i % block.x, (i / block.x) % block.y, i / (block.x * block.y));
         f.lane = i & 63;
         f.wave = i >> 6;
-        f.stack = static_cast<char *>(std::malloc(stack_size));
+        f.stack = stack_pool(i, stack_size);
         f.stack_size = stack_size;
-        if (!f.stack || getcontext(&f.ctx)) fail("fiber setup");
-        f.ctx.uc_stack.ss_sp = f.stack;
-        f.ctx.uc_stack.ss_size = stack_size;
-        f.ctx.uc_link = nullptr;
-        makecontext(&f.ctx, fiber_entry, 0);
+        if (!f.stack) fail("fiber setup");
+        // the frame hostemu_switch pops on the first switch in: control
+        // words, six zeroed registers, then fiber_entry as the return
+        // address, entered with the stack aligned as after a call
+        uint64_t *top = reinterpret_cast<uint64_t *>(f.stack + stack_size) - 2;   // 16-byte aligned
+        top[1] = 0;   // fiber_entry's own (never used) return address
+        top[0] = reinterpret_cast<uint64_t>(&fiber_entry);
+        uint64_t *sp = top - 7;
+        for (int r = 1; r < 7; r++) sp[r] = 0;
+        const uint32_t mxcsr = 0x1F80, fcw = 0x037F;   // power-on defaults
+        sp[0] = mxcsr | (uint64_t)fcw << 32;
+        f.sp = sp;
     }
     for (int left = nt; left > 0;) {
         bool ran = false;
@@ -434,7 +466,7 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
 #if defined(__SANITIZE_ADDRESS__)
             __sanitizer_start_switch_fiber(&m.sched_fake, f.stack, f.stack_size);
 #endif
-            swapcontext(&m.sched, &f.ctx);
+            hostemu_switch(&m.sched_sp, f.sp);
 #if defined(__SANITIZE_ADDRESS__)
             __sanitizer_finish_switch_fiber(m.sched_fake, nullptr, nullptr);
 #endif
@@ -442,14 +474,20 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
         }
         if (!ran && left > 0) fail("deadlock: a barrier or cross-lane operation not reached by every lane");
     }
-    for (auto &f : m.fibers) std::free(f.stack);
     machine() = nullptr;
+}
+
+// launch, recorded in the launch log under `name`
+template <typename K, typename... A>
+void launch_named(const char *name, K kernel, dim3 grid, dim3 block, A... args) {
+    const double t0 = hostemu_now_ms();
+    launch(kernel, grid, block, args...);
+    hostemu_count_launch(name, workgroups(grid), hostemu_now_ms() - t0);
 }
 
 }  // namespace hostemu
 
 #define hipLaunchKernelGGL(kernel, grid, block, shmem, stream, ...) \
-    ((void)(stream), hostemu_count_launch(#kernel, hostemu::workgroups(dim3(grid))), \
-     hostemu::launch(kernel, dim3(grid), dim3(block), __VA_ARGS__))
+    ((void)(stream), hostemu::launch_named(#kernel, kernel, dim3(grid), dim3(block), __VA_ARGS__))
 
 #endif

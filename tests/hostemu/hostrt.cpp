@@ -18,11 +18,44 @@ struct hostemu_event {
     bool recorded;
 };
 
+// The fibers' stack switch (declared in hip/hip_runtime.h): pushes the
+// callee-saved registers and the SSE / x87 control words, stores the stack
+// pointer in *from, loads `to` and pops the same from there.
+asm(R"(
+    .text
+    .globl hostemu_switch
+    .type hostemu_switch, @function
+hostemu_switch:
+    pushq %rbp
+    pushq %rbx
+    pushq %r12
+    pushq %r13
+    pushq %r14
+    pushq %r15
+    subq $8, %rsp
+    stmxcsr (%rsp)
+    fnstcw 4(%rsp)
+    movq %rsp, (%rdi)
+    movq %rsi, %rsp
+    ldmxcsr (%rsp)
+    fldcw 4(%rsp)
+    addq $8, %rsp
+    popq %r15
+    popq %r14
+    popq %r13
+    popq %r12
+    popq %rbx
+    popq %rbp
+    ret
+    .size hostemu_switch, .-hostemu_switch
+)");
+
 namespace {
 
 struct LaunchCount {
     int launches = 0;
     unsigned long long workgroups = 0;
+    double ms = 0.0;
 };
 std::map<std::string, LaunchCount> &launches() {
     static std::map<std::string, LaunchCount> m;
@@ -142,15 +175,19 @@ hipError_t hipGetSymbolAddress(void **p, const void *symbol) {
     return hipSuccess;
 }
 
-void hostemu_count_launch(const char *name, unsigned workgroups) {
+void hostemu_count_launch(const char *name, unsigned workgroups, double ms) {
     LaunchCount &c = launches()[name];
     c.launches++;
     c.workgroups += workgroups;
+    c.ms += ms;
 }
+
+double hostemu_now_ms(void) { return now_ms(); }
 
 void hostemu_print_launches(void) {
     for (const auto &kv : launches())
-        std::printf("launch %s %d %llu\n", kv.first.c_str(), kv.second.launches, kv.second.workgroups);
+        std::printf("launch %s %d %llu %.1f\n", kv.first.c_str(), kv.second.launches, kv.second.workgroups,
+                    kv.second.ms);
 }
 
 }  // extern "C"

@@ -21,6 +21,7 @@ the kernels' indexing (LDS rings, ragged tiles, key splits) under the
 sanitizers; a barrier or cross-lane operation that some lane misses stops
 the run.
 """
+import importlib.util
 import os
 import subprocess
 
@@ -35,6 +36,10 @@ D = 256
 CLANG = "/opt/rocm/lib/llvm/bin/clang++"
 
 pytestmark = pytest.mark.skipif(not os.path.exists(CLANG), reason="ROCm clang not available")
+
+_spec = importlib.util.spec_from_file_location("make_golden", os.path.join(REPO, "tests", "golden", "make_golden.py"))
+MG = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(MG)
 
 
 @pytest.fixture(scope="module")
@@ -53,13 +58,14 @@ def _bf16_valued(a):
 class Emu:
     """A script of library calls and the same calls on the oracle."""
 
-    def __init__(self, tmp, H=8, Hkv=4, max_context=128, window=16, layers=6):
+    def __init__(self, tmp, H=8, Hkv=4, max_context=128, window=16, layers=6, model_dims=None):
         self.dir, self.H, self.Hkv = str(tmp), H, Hkv
         self.cfg = O.Config(max_context=max_context, sliding_window=window, num_heads=H, num_kv_heads=Hkv)
         self.tables = {False: O.rope_table(max_context, 10000.0), True: O.rope_table(max_context, 1e6)}
         self._save("rl.bin", self.tables[False])
         self._save("rg.bin", self.tables[True])
-        self.lines = [f"create {H} {Hkv} {max_context} {window} {layers} 1e-6 rl.bin rg.bin"]
+        dims = " ".join(str(x) for x in model_dims) if model_dims else ""
+        self.lines = [f"create {H} {Hkv} {max_context} {window} {layers} 1e-6 rl.bin rg.bin {dims}"]
         self.caches = {}
         self.checks = []          # (file, expected, label, bar: x RMS, 0 = exact, or an array bound)
         self.k = 0
@@ -142,10 +148,30 @@ class Emu:
         bound = (2.0 ** -16 + K * 2.0 ** -24) * (np.abs(X64) @ np.abs(W64).T) + 1e-30
         self.checks.append((files[2], X64 @ W64.T, f"matmul N={N} M={M} K={K} (max err / bound)", bound))
 
+    def model(self, embed, layers, norm):
+        """The model's tensors as files (absent optional norms: no file)."""
+        self._save("m_embed.bin", embed)
+        self._save("m_norm.bin", norm)
+        for l, lw in enumerate(layers):
+            for name in O.LAYER_TENSORS:
+                if lw[name] is not None:
+                    self._save(f"m_L{l}_{name}.bin", lw[name])
+        self.lines.append("model m_")
+
+    def logits(self, cmd, args, want, label):
+        f = self._name("lg")
+        self.lines.append(f"{cmd} {args} {f}")
+        self.checks.append((f, want, label, 1e-4))
+
     def run(self, **env):
         with open(os.path.join(self.dir, "script.txt"), "w") as f:
             f.write("\n".join(self.lines) + "\n")
-        e = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="print_stacktrace=1")
+        # Stack-use-after-return detection (a fake frame per call on every
+        # fiber) doubles the run time and guards against nothing these
+        # kernels do: they never pass stack addresses out.  The other checks
+        # (heap, globals incl. the LDS arrays, stack bounds, leaks) stay on.
+        e = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:detect_stack_use_after_return=0",
+                 UBSAN_OPTIONS="print_stacktrace=1")
         e.update({k: str(v) for k, v in env.items()})
         res = subprocess.run([EXE, self.dir], capture_output=True, text=True, timeout=1200, env=e)
         assert res.returncode == 0 and "attn_emu: ok" in res.stdout, res.stdout[-2000:] + res.stderr[-4000:]
@@ -158,12 +184,12 @@ class Emu:
                 err = rel_err(got, want) if bar else float(np.abs(got - want).max())
             print(f"[hostemu attn] {label}: {err:.3e}")
             assert err <= bar, (label, err)
-        # "launch <kernel expression> <launches> <workgroups>": workgroups
-        # summed over launches, keyed by the bare kernel name
+        # "launch <kernel expression> <launches> <workgroups> <ms>":
+        # workgroups summed over launches, keyed by the bare kernel name
         launches = {}
         for ln in res.stdout.splitlines():
             if ln.startswith("launch "):
-                expr, count, wgs = ln[len("launch "):].rsplit(" ", 2)
+                expr, count, wgs, _ms = ln[len("launch "):].rsplit(" ", 3)
                 name = expr.strip("()").split("<")[0]
                 c, w = launches.get(name, (0, 0))
                 launches[name] = (c + int(count), w + int(wgs))
@@ -248,3 +274,87 @@ def test_device_entry_and_matmul(built, tmp_path):
     e.matmul(130, 20, 64)
     launches = e.run()
     assert launches["gemm_kernel"][0] == 2, launches
+
+
+# A model of Gemma 3's structure small enough to emulate a token in a few
+# seconds: 6 layers (layer 5 global), 2 query heads over 1 KV head of 256,
+# hidden 128, intermediate 256, vocab 256, an 8-row sliding window, and
+# layer 3 without its optional norms (the forward golden's layout, scaled).
+SMALL = dict(hidden=128, inter=256, vocab=256, layers=6, max_context=32, window=8, heads=2, kv_heads=1)
+
+
+def _forward_model(n):
+    f = SMALL
+    cfg = O.Config(num_layers=f["layers"], max_context=f["max_context"], sliding_window=f["window"],
+                   num_heads=f["heads"], num_kv_heads=f["kv_heads"])
+    Hd, I, V = f["hidden"], f["inter"], f["vocab"]
+    qs, ks = f["heads"] * D, f["kv_heads"] * D
+    embed = MG.weights_bf16(V, Hd, 0xE000)
+    layers = []
+    for l in range(f["layers"]):
+        sd = 0xE100 + 32 * l
+        lw = dict(input_layernorm=MG.norm_bf16(Hd, sd), q_proj=MG.weights_bf16(qs, Hd, sd + 1),
+                  k_proj=MG.weights_bf16(ks, Hd, sd + 2), v_proj=MG.weights_bf16(ks, Hd, sd + 3),
+                  o_proj=MG.weights_bf16(Hd, qs, sd + 4), q_norm=MG.norm_bf16(D, sd + 5),
+                  k_norm=MG.norm_bf16(D, sd + 6), post_attention_layernorm=MG.norm_bf16(Hd, sd + 7),
+                  gate_proj=MG.weights_bf16(I, Hd, sd + 8), up_proj=MG.weights_bf16(I, Hd, sd + 9),
+                  down_proj=MG.weights_bf16(Hd, I, sd + 10), pre_feedforward_layernorm=MG.norm_bf16(Hd, sd + 11),
+                  post_feedforward_layernorm=MG.norm_bf16(Hd, sd + 12))
+        if l == 3:
+            for k in ("q_norm", "k_norm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                      "post_feedforward_layernorm"):
+                lw[k] = None
+        layers.append(lw)
+    norm = MG.norm_bf16(Hd, 0xEF00)
+    tokens = np.random.default_rng(0xE0E0).integers(0, V, n).astype(np.int32)
+    logits, _ = O.forward_seq(cfg, Hd, I, tokens, embed, layers, norm)
+    return f, embed, layers, norm, tokens, logits
+
+
+def _emu_for(tmp_path, f):
+    return Emu(tmp_path, H=f["heads"], Hkv=f["kv_heads"], max_context=f["max_context"], window=f["window"],
+               layers=f["layers"], model_dims=(f["hidden"], f["inter"], f["vocab"]))
+
+
+# residual_kernel launches per token: fold 0 runs the two steps of every
+# layer as kernels; fold 1 moves the step before layers 1-5's Q/K/V launch
+# into it; fold 3 also the step before every gate/up launch (the final norm
+# after the last layer stays a kernel)
+RESIDUAL_PER_TOKEN = {0: 12, 1: 7, 3: 1}
+
+
+@pytest.mark.parametrize("fold", [0, 1, 3])
+def test_token_forward(built, tmp_path, fold):
+    """g3attn_forward_device through every token-path kernel (embedding,
+    norms, the fused Q/K/V GEMV with or without the residual prologue,
+    decode, o_proj, GEGLU, down_proj, tied logits): each token's logits
+    against the oracle's gemma3_transformer_forward
+    (gemma3_transformer.c:396-512), for each residual-fold mode.  Fold 1
+    (the default) runs 11 tokens, wrapping the 8-row window; the others 3.
+    Bar 1e-4 x RMS, as on the GPU."""
+    n = 11 if fold == 1 else 3
+    f, embed, layers, norm, tokens, want = _forward_model(n)
+    e = _emu_for(tmp_path, f)
+    e.model(embed, layers, norm)
+    for i, t in enumerate(tokens):
+        e.logits("forward_device", f"{int(t)} {i}", want[i], f"forward_device token {i} fold={fold}")
+    launches = e.run(G3ATTN_FORWARD_FOLD=fold)
+    assert launches["residual_kernel"][0] == n * RESIDUAL_PER_TOKEN[fold], launches
+
+
+def test_upload_batched_prefill_then_decode(built, tmp_path):
+    """g3attn_upload_weights from host tensors, g3attn_prefill_tokens over 16
+    tokens (the batched path: MFMA GEMMs in plain and GEGLU modes, per-row
+    kernels, the prefill attention, ring writes past the window) giving the
+    last token's logits, then g3attn_forward_token continuing from the cache
+    it wrote."""
+    n = 17
+    f, embed, layers, norm, tokens, want = _forward_model(n)
+    e = _emu_for(tmp_path, f)
+    e.model(embed, layers, norm)
+    e.lines.append("upload")
+    e._save("tok.bin", tokens[:n - 1].astype(np.int32))
+    e.logits("prefill_tokens", f"{n - 1} tok.bin 0", want[n - 2], f"prefill_tokens n={n - 1} last logits")
+    e.logits("forward_token", f"{int(tokens[n - 1])} {n - 1}", want[n - 1], f"forward_token {n - 1}")
+    launches = e.run()
+    assert launches["gemm_kernel"][0] > 0 and launches["rows_kernel"][0] > 0, launches

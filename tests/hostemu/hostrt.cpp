@@ -68,10 +68,11 @@ double now_ms() {
 }
 
 void *aligned(size_t bytes) {
-    // 256-byte alignment, as hipMalloc gives; at least one byte so every
-    // allocation is distinct
-    const size_t n = (bytes + 255) / 256 * 256;
-    return std::aligned_alloc(256, n ? n : 256);
+    // 256-byte alignment, as hipMalloc gives, and exactly the requested size
+    // (at least one byte), so AddressSanitizer flags any access past it even
+    // where the GPU allocator's granularity would have hidden it
+    void *p = nullptr;
+    return posix_memalign(&p, 256, bytes ? bytes : 1) == 0 ? p : nullptr;
 }
 
 }  // namespace

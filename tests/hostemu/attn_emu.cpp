@@ -17,6 +17,12 @@
 //   prefill_device ...                          (same, device pointers)
 //   decode layer pos q k v q_norm k_norm out
 //   matmul N M K W X C                          (g3attn_matmul_bf16_device)
+//   gqa H Hkv seq q k v mask|- out              (g3attn_gqa, host pointers)
+//   gqa_noalloc H Hkv seq q k v mask|- out      (device copies, null stream)
+//   matvec M K A x y                            (g3attn_matvec_bf16, host)
+//   matvec_device M K A x y                     (g3attn_matvec_bf16_device)
+//   kv_append layer start n K V k_norm|-
+//   layer_attention layer pos hidden x wq wk wv wo q_norm|- k_norm|- out
 //   model prefix     the model's bf16 tensors from prefix + "embed.bin",
 //                    "norm.bin" and "L<l>_<tensor>.bin" (a missing file is a
 //                    NULL tensor), kept in host memory and as device copies
@@ -247,6 +253,83 @@ int main(int argc, char **argv) {
             hipFree(dX);
             hipFree(dC);
             write_bin(cf, C.data(), C.size());
+        } else if (cmd == "gqa" || cmd == "gqa_noalloc") {
+            int h, hkv, seq;
+            std::string qf, kf, vf, mf, of;
+            in >> h >> hkv >> seq >> qf >> kf >> vf >> mf >> of;
+            if (!in) die("bad " + cmd + " line");
+            const auto q = read_bin<float>(qf, (size_t)h * D);
+            const auto k = read_bin<float>(kf, (size_t)seq * hkv * D);
+            const auto v = read_bin<float>(vf, (size_t)seq * hkv * D);
+            std::vector<float> mask;
+            if (mf != "-") mask = read_bin<float>(mf, (size_t)seq);
+            std::vector<float> out((size_t)h * D, -12345.0f);
+            const float scale = 0.0625f;
+            if (cmd == "gqa") {
+                g3attn_gqa(out.data(), q.data(), k.data(), v.data(), h, hkv, seq, (int)D, scale,
+                           mask.empty() ? nullptr : mask.data(), nullptr);
+                if (out[0] == -12345.0f) check(-1, cmd);   // g3attn_gqa reports failure only by leaving out as is
+            } else {
+                float *dq = to_device(q), *dk = to_device(k), *dv = to_device(v), *dout = to_device(out);
+                float *dm = mask.empty() ? nullptr : to_device(mask);
+                check(g3attn_gqa_noalloc(dout, dq, dk, dv, h, hkv, seq, (int)D, scale, dm, nullptr), cmd);
+                hipDeviceSynchronize();
+                hipMemcpy(out.data(), dout, out.size() * sizeof(float), hipMemcpyDeviceToHost);
+                for (void *p : {(void *)dq, (void *)dk, (void *)dv, (void *)dout, (void *)dm}) hipFree(p);
+            }
+            write_bin(of, out.data(), out.size());
+        } else if (cmd == "matvec" || cmd == "matvec_device") {
+            int M, K;
+            std::string af, xf, yf;
+            in >> M >> K >> af >> xf >> yf;
+            if (!in) die("bad " + cmd + " line");
+            const auto A = read_bin<uint16_t>(af, (size_t)M * K);
+            const auto x = read_bin<float>(xf, (size_t)K);
+            std::vector<float> y((size_t)M, -12345.0f);
+            if (cmd == "matvec") {
+                g3attn_matvec_bf16(y.data(), A.data(), x.data(), M, K, nullptr);
+                if (M > 0 && y[0] == -12345.0f) check(-1, cmd);
+            } else {
+                if (!ctx) die("matvec_device needs a context");
+                uint16_t *dA = to_device(A);
+                float *dx = to_device(x), *dy = to_device(y);
+                check(g3attn_matvec_bf16_device(ctx, dy, dA, dx, M, K), cmd);
+                check(g3attn_synchronize(ctx), "g3attn_synchronize");
+                hipMemcpy(y.data(), dy, y.size() * sizeof(float), hipMemcpyDeviceToHost);
+                for (void *p : {(void *)dA, (void *)dx, (void *)dy}) hipFree(p);
+            }
+            write_bin(yf, y.data(), y.size());
+        } else if (cmd == "kv_append") {
+            int layer, start, n;
+            std::string kf, vf, kn;
+            in >> layer >> start >> n >> kf >> vf >> kn;
+            if (!in || !ctx) die("bad kv_append line");
+            const auto K = read_bin<float>(kf, (size_t)n * Hkv * D);
+            const auto V = read_bin<float>(vf, (size_t)n * Hkv * D);
+            const Gain gk = read_gain(kn);
+            check(g3attn_kv_append(ctx, layer, start, n, K.data(), V.data(), gk.ptr()), cmd);
+        } else if (cmd == "layer_attention") {
+            int layer, pos, hid;
+            std::string xf, wqf, wkf, wvf, wof, qn, kn, of;
+            in >> layer >> pos >> hid >> xf >> wqf >> wkf >> wvf >> wof >> qn >> kn >> of;
+            if (!in || !ctx) die("bad layer_attention line");
+            const size_t qs = (size_t)H * D, ks = (size_t)Hkv * D;
+            const auto x = read_bin<float>(xf, (size_t)hid);
+            const auto wq = read_bin<uint16_t>(wqf, qs * hid), wk = read_bin<uint16_t>(wkf, ks * hid);
+            const auto wv = read_bin<uint16_t>(wvf, ks * hid), wo = read_bin<uint16_t>(wof, hid * qs);
+            const Gain gq = read_gain(qn), gk = read_gain(kn);
+            std::vector<float> out((size_t)hid, -12345.0f);
+            float *dx = to_device(x), *dout = to_device(out);
+            uint16_t *dq = to_device(wq), *dk = to_device(wk), *dv = to_device(wv), *dw = to_device(wo);
+            uint16_t *dqn = gq.v.empty() ? nullptr : to_device(gq.v);
+            uint16_t *dkn = gk.v.empty() ? nullptr : to_device(gk.v);
+            check(g3attn_layer_attention_device(ctx, layer, pos, dx, dq, dk, dv, dw, dqn, dkn, dout), cmd);
+            check(g3attn_synchronize(ctx), "g3attn_synchronize");
+            hipMemcpy(out.data(), dout, out.size() * sizeof(float), hipMemcpyDeviceToHost);
+            for (void *p : {(void *)dx, (void *)dout, (void *)dq, (void *)dk, (void *)dv, (void *)dw, (void *)dqn,
+                            (void *)dkn})
+                hipFree(p);
+            write_bin(of, out.data(), out.size());
         } else if (cmd == "model") {
             std::string prefix;
             in >> prefix;

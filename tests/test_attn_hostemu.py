@@ -148,6 +148,70 @@ class Emu:
         bound = (2.0 ** -16 + K * 2.0 ** -24) * (np.abs(X64) @ np.abs(W64).T) + 1e-30
         self.checks.append((files[2], X64 @ W64.T, f"matmul N={N} M={M} K={K} (max err / bound)", bound))
 
+    def gqa(self, h, hkv, seq, masked=False, noalloc=False):
+        """g3attn_gqa / _noalloc against the oracle's gemma3_gqa (1e-4 x RMS)."""
+        q = self.rng.standard_normal(h * D).astype(np.float32)
+        k = self.rng.standard_normal(seq * hkv * D).astype(np.float32)
+        v = self.rng.standard_normal(seq * hkv * D).astype(np.float32)
+        files = [self._name(s) for s in ("gq", "gk", "gv", "go")]
+        for f, a in zip(files, (q, k, v)):
+            self._save(f, a)
+        mask, mf = None, "-"
+        if masked:
+            mask = (self.rng.standard_normal(seq) * 2).astype(np.float32)
+            mask[self.rng.random(seq) < 0.3] = -1e9
+            mf = self._name("gm")
+            self._save(mf, mask)
+        cmd = "gqa_noalloc" if noalloc else "gqa"
+        self.lines.append(f"{cmd} {h} {hkv} {seq} {files[0]} {files[1]} {files[2]} {mf} {files[3]}")
+        want = O.gqa(q, k, v, h, hkv, seq, mask=mask)
+        self.checks.append((files[3], want, f"{cmd} {h}/{hkv} seq={seq} mask={masked}", 1e-4))
+
+    def matvec(self, M, K, device=False):
+        """g3attn_matvec_bf16 (host) / _device against gemma3_matvec_bf16 (1e-5 x RMS)."""
+        A = (_bf16_valued(self.rng.standard_normal((M, K)) * 0.05).view(np.uint32) >> 16).astype(np.uint16)
+        x = self.rng.standard_normal(K).astype(np.float32)
+        files = [self._name(s) for s in ("mA", "mx", "my")]
+        self._save(files[0], A)
+        self._save(files[1], x)
+        cmd = "matvec_device" if device else "matvec"
+        self.lines.append(f"{cmd} {M} {K} {files[0]} {files[1]} {files[2]}")
+        self.checks.append((files[2], O.matvec_bf16(A, x), f"{cmd} M={M} K={K}", 1e-5))
+
+    def kv_append(self, layer, start, n, norm=True):
+        """g3attn_kv_append; the oracle's cache gets the K-normed, rotated rows
+        in ring order (cache_kv, gemma3_transformer.c:236-251)."""
+        _, K, V = self.inputs(n)
+        _, gk, _, nk = self.gains(norm)
+        kf, vf = self._name("aK"), self._name("aV")
+        self._save(kf, K)
+        self._save(vf, V)
+        self.lines.append(f"kv_append {layer} {start} {n} {kf} {vf} {nk}")
+        Kr = K.reshape(n, self.Hkv, D).copy()
+        O.norm_rope_batch(Kr, self.tables[O.is_global_layer(layer)], start, gk)
+        Kc, Vc = self._cache(layer)
+        for i in range(n):
+            p = start + i
+            slot = p if O.is_global_layer(layer) else p % self.cfg.sliding_window
+            Kc[slot] = Kr[i].reshape(-1)
+            Vc[slot] = V[i]
+
+    def layer_attention(self, layer, pos, hidden, norm=True):
+        """g3attn_layer_attention_device against the oracle's layer_attention
+        (gemma3_transformer.c:258-356; 1e-4 x RMS)."""
+        qs, ks = self.H * D, self.Hkv * D
+        w = [(_bf16_valued(self.rng.standard_normal(r * c) * 0.05).view(np.uint32) >> 16).astype(np.uint16)
+             .reshape(r, c) for r, c in ((qs, hidden), (ks, hidden), (ks, hidden), (hidden, qs))]
+        x = self.rng.standard_normal(hidden).astype(np.float32)
+        gq, gk, nq, nk = self.gains(norm)
+        files = [self._name(s) for s in ("lx", "lwq", "lwk", "lwv", "lwo", "lo")]
+        for f, a in zip(files, [x] + w):
+            self._save(f, a)
+        self.lines.append(f"layer_attention {layer} {pos} {hidden} " + " ".join(files[:5]) + f" {nq} {nk} {files[5]}")
+        Kc, Vc = self._cache(layer)
+        want = O.layer_attention(self.cfg, layer, pos, x, *w, Kc, Vc, self.tables[O.is_global_layer(layer)], gq, gk)
+        self.checks.append((files[5], want, f"layer_attention layer={layer} pos={pos}", 1e-4))
+
     def model(self, embed, layers, norm):
         """The model's tensors as files (absent optional norms: no file)."""
         self._save("m_embed.bin", embed)
@@ -274,6 +338,47 @@ def test_device_entry_and_matmul(built, tmp_path):
     e.matmul(130, 20, 64)
     launches = e.run()
     assert launches["gemm_kernel"][0] == 2, launches
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(8, 4), (4, 4), (8, 2)])
+def test_gqa_entry_points(built, tmp_path, heads, kv_heads):
+    """g3attn_gqa (the gemma3_gqa drop-in, host pointers, a process-wide
+    context) with and without an additive mask, and g3attn_gqa_noalloc (device
+    buffers, the static scratch) on two calls in a row, the second shorter."""
+    e = Emu(tmp_path, H=heads, Hkv=kv_heads)
+    e.gqa(heads, kv_heads, 300)
+    e.gqa(heads, kv_heads, 77, masked=True)
+    e.gqa(heads, kv_heads, 300, masked=True, noalloc=True)
+    e.gqa(heads, kv_heads, 40, noalloc=True)
+    e.run()
+
+
+def test_matvec_entry_points(built, tmp_path):
+    """g3attn_matvec_bf16 (the gemma3_matvec_bf16 drop-in, host pointers) and
+    the device form, at a Q-projection shape and a ragged one."""
+    e = Emu(tmp_path)
+    e.matvec(70, 2560)
+    e.matvec(33, 100)
+    e.matvec(70, 2560, device=True)
+    e.matvec(5, 40, device=True)
+    e.run()
+
+
+def test_kv_append_and_layer_attention(built, tmp_path):
+    """g3attn_kv_append filling a global and a local layer's cache (the local
+    batch longer than its 16-row ring), decode steps over what it wrote, and
+    the whole layer_attention on device buffers for three tokens (the
+    context's hidden size, 256, sizes x and the projections)."""
+    e = Emu(tmp_path, model_dims=(256, 512, 256))
+    e.kv_append(5, 0, 50)
+    e.decode(5, 50)
+    e.kv_append(0, 0, 20, norm=False)
+    e.decode(0, 20, norm=False)
+    e.check_cache(5, 0, 51)
+    e.check_cache(0, 0, 16)
+    for pos in range(3):
+        e.layer_attention(1, pos, 256)
+    e.run()
 
 
 # A model of Gemma 3's structure small enough to emulate a token in a few

@@ -146,8 +146,9 @@ struct g3attn_ctx {
     int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
     int n_cu;       /* compute units of the device */
-    /* decode: non-temporal cache loads on 1 every layer, 2 global layers only
-     * (the default), 0 none (G3ATTN_DECODE_NT) */
+    /* decode: non-temporal cache loads on 1 every layer, 2 global layers
+     * only, and every layer inside the token forward (the default), 0 none
+     * (G3ATTN_DECODE_NT) */
     int nt_loads;
     /* token forward: residual steps folded into the next GEMV's prologue
      * (bit 0: into the Q/K/V launch, bit 1: into the gate/up launch;
@@ -527,9 +528,11 @@ int g3attn_upload_rope(g3attn_ctx *c, const float *rope_local, const float *rope
     return G3_OK;
 }
 
-int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
-                         const float *v, const uint16_t *q_norm, const uint16_t *k_norm,
-                         float *attn_out) {
+/* One decode step; in_forward: called by the token forward (cache policy
+ * below). */
+static int decode_enqueue(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
+                          const float *v, const uint16_t *q_norm, const uint16_t *k_norm,
+                          float *attn_out, int in_forward) {
     if (!check_layer(c, layer, "g3attn_decode") || !check_rope(c, "g3attn_decode")) return G3_ERR_INVALID_ARG;
     if (!q || !k || !v || !attn_out || pos < 0) {
         set_err("g3attn_decode: null buffer or pos < 0");
@@ -569,14 +572,19 @@ int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, cons
     a.out = attn_out;
     a.ws_acc = c->ws_acc;
     a.ws_ml = c->ws_ml;
-    /* A global layer streams its whole cache once per token: non-temporal
-     * loads keep it from evicting everything else.  A local layer re-reads
-     * a window that changes by one row per token, so its rows are loaded
-     * normally and the caches may keep them (29 + 5 stack at 131071:
-     * 1089 -> 1079 us per token; configs[0] 9.4 -> 8.9 us).  The
-     * non-temporal loads address a KV head's rows with 32-bit byte offsets:
-     * heads of 4 GiB or more (max_context >= 4M) take plain loads. */
-    a.nt_loads = (c->nt_loads == 1 || (c->nt_loads == 2 && is_global)) &&
+    /* Cache policy of the K/V loads (G3ATTN_DECODE_NT = 2).  A global layer
+     * streams its whole cache once per token: non-temporal loads keep it
+     * from evicting everything else.  Called for attention alone, a local
+     * layer re-reads a window that changes by one row per token, so its rows
+     * are loaded normally and the memory-side cache keeps them (29 + 5 stack
+     * at 131071: 1089 -> 1079 us per token; configs[0] 9.4 -> 8.9 us).
+     * Inside the token forward the 28-29 windows (235 MB) would instead push
+     * out the norm rows the residual steps re-read every token (local
+     * decode -0.4 us, residual step +0.5 us: 2.10 -> 2.12 ms per token), so
+     * there every layer streams non-temporally.  The non-temporal loads
+     * address a KV head's rows with 32-bit byte offsets: heads of 4 GiB or
+     * more (max_context >= 4M) take plain loads. */
+    a.nt_loads = (c->nt_loads == 1 || (c->nt_loads == 2 && (is_global || in_forward))) &&
                  (size_t)c->rows[layer] * D * sizeof(float) < ((size_t)1 << 32);
     hipSetDevice(c->device);
     int rc = prof_slot(c, 0, &a.ev0, &a.ev1);
@@ -584,6 +592,12 @@ int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, cons
     rc = g3k_decode(&a, 1, c->stream);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_decode launch");
     return G3_OK;
+}
+
+int g3attn_decode_device(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
+                         const float *v, const uint16_t *q_norm, const uint16_t *k_norm,
+                         float *attn_out) {
+    return decode_enqueue(c, layer, pos, q, k, v, q_norm, k_norm, attn_out, 0);
 }
 
 int g3attn_decode(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
@@ -1235,7 +1249,7 @@ static int forward_enqueue(g3attn_ctx *c, const g3attn_weights *w, int token_id,
         } else if ((rc = g3attn_qkv_proj_device(c, xn, lw->q_proj, lw->k_proj, lw->v_proj, q, k, v))) {
             return rc;
         }
-        if ((rc = g3attn_decode_device(c, l, pos, q, k, v, lw->q_norm, lw->k_norm, attn))) return rc;
+        if ((rc = decode_enqueue(c, l, pos, q, k, v, lw->q_norm, lw->k_norm, attn, 1))) return rc;
         if ((rc = gemv(c, proj, lw->o_proj, attn, hid, qs))) return rc;
         /* layer_mlp (:480-487, 369-388): gate and up GEMVs with gelu(gate) * up,
          * after the post-attention norm, residual add and pre-feedforward

@@ -1,8 +1,10 @@
 """Randomised sessions on the GPU against the oracle: breadth over the
 combinations the targeted tests pick one at a time.
 
-Each seed draws a head layout (GQA group 1, 2 or 4), a sliding window (32,
-64 or 1024) and then drives one local and one global layer of a context
+Each seed draws a head layout (GQA group 1, 2 or 4), a sliding window (1, 7,
+32, 64, 100 or 1024), a max_context (1536, or 1000: not a multiple of the
+64-key staging grain) and then drives one local and one global layer of a
+context
 through a random sequence of calls from position 0: prefill chunks of 1 to
 200 tokens (chunks longer than the window, chunks whose history wraps the
 ring) and runs of 1 to 3 decode steps.  Every call draws bf16-valued or
@@ -22,7 +24,6 @@ pytestmark = pytest.mark.gpu
 
 G = g3attn()
 D = 256
-MAXC = 1536
 
 
 def _bf16(a):
@@ -38,7 +39,8 @@ def _gain(rng):
 def test_random_session(seed):
     rng = np.random.default_rng(0x5EED00 + seed)
     heads, kv_heads = [(8, 4), (4, 4), (8, 2)][seed % 3]
-    window = [32, 64, 1024][(seed // 3) % 3]
+    window = [32, 64, 1024, 1, 7, 100][(seed // 3) % 6]
+    MAXC = 1000 if seed % 2 else 1536
     cfg_o = O.Config(max_context=MAXC, sliding_window=window, num_heads=heads, num_kv_heads=kv_heads)
     tables = {False: O.rope_table(MAXC, 10000.0), True: O.rope_table(MAXC, 1e6)}
     cfg = G.default_config(max_context=MAXC, sliding_window=window, num_layers=6, num_heads=heads,
@@ -54,7 +56,7 @@ def test_random_session(seed):
             Kc = np.zeros((rows, ks), np.float32)
             Vc = np.zeros((rows, ks), np.float32)
             pos = 0
-            limit = int(rng.integers(300, 900))
+            limit = int(rng.integers(300, 900))   # < MAXC
             while pos < limit:
                 fp32 = rng.random() < 0.3
                 conv = (lambda a: a.astype(np.float32)) if fp32 else _bf16
@@ -90,5 +92,5 @@ def test_random_session(seed):
             k_got, v_got = ctx.kv_read(layer, 0, used)
             assert rel_err(k_got, Kc[:used]) < 1e-5, (seed, layer)
             assert np.array_equal(v_got, Vc[:used]), (seed, layer)
-    print(f"[sweep seed={seed}] heads={heads}/{kv_heads} window={window} calls={n_calls} "
+    print(f"[sweep seed={seed}] heads={heads}/{kv_heads} window={window} max_context={MAXC} calls={n_calls} "
           f"worst prefill={worst['prefill']:.2e} decode={worst['decode']:.2e}", flush=True)

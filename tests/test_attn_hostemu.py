@@ -381,6 +381,32 @@ def test_kv_append_and_layer_attention(built, tmp_path):
     e.run()
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_sessions(built, tmp_path, seed):
+    """Random sequences of prefill chunks (1-48 tokens) and decode runs on a
+    local and a global layer, with odd windows (1, 7, 32) and a max_context
+    off the 64-key staging grain (200), bf16 or fp32 inputs, QK-norm or
+    none: the host code's ring and staging arithmetic under the sanitizers
+    on the combinations the GPU sweep draws at larger sizes."""
+    rng = np.random.default_rng(0xE5EED + seed)
+    window = [1, 7, 32][seed % 3]
+    e = Emu(tmp_path, H=[8, 4, 8][seed % 3], Hkv=[4, 4, 2][seed % 3], max_context=200, window=window)
+    for layer in (1, 5):
+        pos = 0
+        while pos < 90:
+            norm, bf16 = bool(rng.random() < 0.7), bool(rng.random() < 0.7)
+            if rng.random() < 0.5:
+                n = int(rng.integers(1, 49))
+                e.prefill(layer, pos, n, norm=norm, bf16=bf16)
+                pos += n
+            else:
+                for _ in range(int(rng.integers(1, 3))):
+                    e.decode(layer, pos, norm=norm)
+                    pos += 1
+        e.check_cache(layer, 0, min(pos, window if layer == 1 else pos))
+    e.run()
+
+
 # A model of Gemma 3's structure small enough to emulate a token in a few
 # seconds: 6 layers (layer 5 global), 2 query heads over 1 KV head of 256,
 # hidden 128, intermediate 256, vocab 256, an 8-row sliding window, and

@@ -121,6 +121,33 @@ def test_decode_gqa_groups(n_heads, n_kv):
         ctx.close()
 
 
+def test_load_forms_agree(monkeypatch):
+    """The cache-policy modes of the fused decode (G3ATTN_DECODE_NT: 0 plain
+    loads, 1 non-temporal buffer loads on every layer, 2 the default, plain
+    on local layers) change how K/V rows are fetched, never what is
+    computed: outputs and cache rows are bit-identical across the modes, and
+    each matches the oracle.  Local layers inside the window and across the
+    ring wrap, a global layer, groups 2 and 4."""
+    for n_heads, n_kv in ((8, 4), (8, 2)):
+        outs = {}
+        for mode in (0, 1, 2):
+            monkeypatch.setenv("G3ATTN_DECODE_NT", str(mode))
+            ctx = _ctx(4096, num_layers=6, n_heads=n_heads, n_kv=n_kv)
+            try:
+                got = []
+                for layer, pos in ((0, 700), (1, 2500), (5, 3000)):
+                    case = DecodeCase(14, layer=layer, pos=pos, max_context=4096, n_heads=n_heads, n_kv=n_kv)
+                    _check(case, ctx, f"nt{mode}")
+                    got.append(case.gpu(ctx))   # again, on the cache the first call completed
+                    got.append(np.concatenate(ctx.kv_read(layer, 0, 64)))
+                outs[mode] = got
+            finally:
+                ctx.close()
+        for mode in (1, 2):
+            for a, b in zip(outs[0], outs[mode]):
+                assert np.array_equal(a, b), (n_heads, n_kv, mode)
+
+
 def test_tables_uploaded_after_create():
     """A context created without RoPE tables (the backend hook's init, which
     takes none) refuses attention calls until g3attn_upload_rope, then matches

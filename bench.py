@@ -215,7 +215,7 @@ def cpu_baseline(L=8192, reps=20):
         t = O.rope_table(L, 1e6, use_ref=True)
         O.norm_rope_batch(K, t, 0, zn)  # rows as the cache holds them
         zp = zn.ctypes.data_as(C.c_void_p)
-        sec = O.ref().ref_time_decode(q, k, v, zp, zp, K, V, t, HQ, HKV, 5, pos, L, 1024, 3, reps)
+        sec = O.ref_timing().ref_time_decode(q, k, v, zp, zp, K, V, t, HQ, HKV, 5, pos, L, 1024, 3, reps)
     else:
         t = O.rope_table(L, 1e6)
         O.norm_rope_batch(K, t, 0, zn)
@@ -239,7 +239,9 @@ def cpu_baseline(L=8192, reps=20):
         "sample": (f"median of {reps} decode steps (configs[1]: L={L}, pos {pos}) after 3 warm-up, "
                    f"{sec * 1e6:.0f} us/step, 1 thread ({cpu_model}; nproc {os.cpu_count()}); "
                    "reference gemma3_kernels.c + gemma3_transformer.c built with "
-                   "-O3 -march=x86-64-v3 -ffast-math, no BLAS (cblas.h absent)"),
+                   f"-O3 -march={O.ref_timing_build()} -ffast-math (the reference's make fast flags; "
+                   "x86-64-v4 is the AVX-512 width its -march=native gives on this host), "
+                   "no BLAS (cblas.h absent)"),
     }
 
 
@@ -261,12 +263,14 @@ def cpu_gemv_baseline(hid=2560, layers=8, reps=3):
     shapes = ((QS, hid), (KS, hid), (KS, hid), (hid, QS))
     mats = [[np.resize(np.roll(pool, 997 * (4 * l + j)), sh) for j, sh in enumerate(shapes)] for l in range(layers)]
     xs = [np.random.default_rng(8).standard_normal(sh[1]).astype(np.float32) for sh in shapes]
+    R = O.ref_timing()
+    ys = [np.empty(sh[0], np.float32) for sh in shapes]
     ts = []
     for r in range(reps + 1):
         a = time.perf_counter()
         for lm in mats:
-            for m, x in zip(lm, xs):
-                O.matvec_bf16(m, x, use_ref=True)
+            for m, x, y in zip(lm, xs, ys):
+                R.ref_matvec_bf16(y, m, x, m.shape[0], m.shape[1])
         if r:
             ts.append((time.perf_counter() - a) / layers)
     sec = float(np.median(ts))
@@ -274,7 +278,7 @@ def cpu_gemv_baseline(hid=2560, layers=8, reps=3):
     return {"value": round(byts / sec / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "reference",
             "sample": f"median of {reps} passes over {layers} distinct layers' four projection matrices "
                       f"({layers * byts / 1e6:.0f} MB): {sec * 1e3:.2f} ms per layer, gemma3_matvec_bf16, "
-                      "1 thread"}
+                      f"1 thread, -march={O.ref_timing_build()}"}
 
 
 def cpu_forward_baseline(HW, cfg, pos, n_tokens=2):
@@ -289,7 +293,7 @@ def cpu_forward_baseline(HW, cfg, pos, n_tokens=2):
     for l in range(L):
         for j, n in enumerate(names):
             ptrs[13 * l + j] = getattr(HW.layers[l], n)
-    sec = O.ref().ref_time_forward(HW.embed_tokens, ptrs, HW.norm, cfg.vocab_size, cfg.hidden_size,
+    sec = O.ref_timing().ref_time_forward(HW.embed_tokens, ptrs, HW.norm, cfg.vocab_size, cfg.hidden_size,
                                    cfg.intermediate_size, L, cfg.num_heads, cfg.num_kv_heads,
                                    cfg.max_context, cfg.sliding_window, pos, n_tokens)
     return None if sec <= 0 else sec
@@ -313,13 +317,14 @@ def cpu_prefill_baseline():
     zn = O.zero_norm()
     a = time.perf_counter()
     if kind == "reference":
-        O.ref_prefill(cfg, layer, 0, Q, K, V, Kc, Vc, t, zn, zn)
+        O.ref_prefill(cfg, layer, 0, Q, K, V, Kc, Vc, t, zn, zn, lib=O.ref_timing())
     else:
         O.prefill(cfg, layer, 0, Q, K, V, Kc, Vc, t, zn, zn, threads=1)
     sec = time.perf_counter() - a
     flops = prefill_flops(n, 1024)
     return {"value": round(flops / sec / 1e12, 6), "unit": "algorithmic TFLOP/s", "cores": 1,
-            "kind": kind, "sample": f"configs[2] in full (N={n}, window 1024), one run: {sec:.2f} s"}
+            "kind": kind, "sample": f"configs[2] in full (N={n}, window 1024), one run: {sec:.2f} s"
+                                    + (f", -march={O.ref_timing_build()}" if kind == "reference" else "")}
 
 
 def main():
@@ -649,14 +654,15 @@ def main():
                 extra["forward_token_pos8191"]["cpu_baseline"] = {
                     "value": round(1.0 / s_hi, 3), "unit": "tokens/s", "cores": 1, "kind": "reference",
                     "sample": f"gemma3_transformer_forward, median of 2 tokens at pos 8190-8191 after one "
-                              f"warm-up token: {s_hi:.2f} s per token, 1 thread, no BLAS, same weights"}
+                              f"warm-up token: {s_hi:.2f} s per token, 1 thread, no BLAS, same weights, "
+                              f"-march={_oracle().ref_timing_build()}"}
             if s_lo:
                 extra["cpu_prefill_model_token_loop"] = {
                     "value": round(1.0 / s_lo, 3), "unit": "tokens/s", "cores": 1, "kind": "reference",
                     "sample": f"the non-BLAS reference prefill is this token loop "
                               f"(gemma3_transformer.c:814-821): gemma3_transformer_forward at pos "
-                              f"1023-1024, {s_lo:.2f} s per token, 1 thread (the BLAS build's batched "
-                              f"prefill needs cblas.h, absent)"}
+                              f"1023-1024, {s_lo:.2f} s per token, 1 thread, -march={_oracle().ref_timing_build()} "
+                              f"(the BLAS build's batched prefill needs cblas.h, absent)"}
         del host
 
         # the batched prefill (MFMA projections + the prefill attention kernel)

@@ -7,7 +7,8 @@ this module.  It loads
   (g3_oracle.c; reference lines cited there), and
 * ``oracle/_ref/libg3ref.so`` - the real reference sources compiled in place
   (ref_harness.c), present only where ``/root/reference`` was available at
-  build time.
+  build time, and ``libg3ref_v4.so``, the same at -march=x86-64-v4 (AVX-512),
+  which ``ref_timing()`` picks for bench.py's CPU baseline on hosts that run it.
 
 Arrays are numpy float32 / uint16, C-contiguous; shapes follow the reference:
 q [H_q*d], k/v [H_kv*d], caches [rows][H_kv][d].
@@ -23,6 +24,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "lib", "libg3oracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libg3ref.so")
+REF_V4_SO = os.path.join(HERE, "_ref", "libg3ref_v4.so")
+# x86-64-v4: AVX-512 F, BW, CD, DQ and VL on top of x86-64-v3
+_V4_FLAGS = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
@@ -139,46 +143,83 @@ def have_ref() -> bool:
     return os.path.exists(REF_SO)
 
 
+def _host_has_v4() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return all(x in flags for x in _V4_FLAGS)
+    except OSError:
+        pass
+    return False
+
+
+def ref_timing_build() -> str:
+    """Which reference build ref_timing() loads: "x86-64-v4" where this host
+    runs AVX-512 and the build exists, else "x86-64-v3"."""
+    return "x86-64-v4" if os.path.exists(REF_V4_SO) and _host_has_v4() else "x86-64-v3"
+
+
+_ref_v4 = None
+
+
+def ref_timing():
+    """The reference build for timing on this host: the x86-64-v4 one (the
+    vector width the reference's -march=native gives on an AVX-512 host)
+    where it runs, else ref().  Parity checks use ref()."""
+    global _ref_v4
+    if ref_timing_build() == "x86-64-v3":
+        return ref()
+    if _ref_v4 is None:
+        _ref_v4 = _bind_ref(C.CDLL(REF_V4_SO))
+    return _ref_v4
+
+
 def ref():
     """The real reference kernels (oracle/_ref); raises if not built here."""
     global _ref
     if _ref is None:
         if not have_ref():
             raise RuntimeError(f"reference harness not built: {REF_SO}")
-        R = C.CDLL(REF_SO)
-        R.ref_rope_precompute.argtypes = [_f32p, C.c_int, C.c_int, C.c_float]
-        R.ref_rope_apply.argtypes = [_f32p, _f32p, C.c_int, C.c_int]
-        R.ref_rmsnorm_bf16.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_float]
-        R.ref_softmax.argtypes = [_f32p, C.c_int]
-        R.ref_causal_mask.argtypes = [_f32p, C.c_int, C.c_int]
-        R.ref_gqa.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
-                              C.c_float, C.c_void_p, C.c_void_p]
-        R.ref_layer_decode.argtypes = [_f32p, C.c_void_p, C.c_void_p, _f32p, _f32p, _f32p,
-                                       C.c_void_p, C.c_void_p, _f32p, _f32p, _f32p, C.c_int,
-                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
-        R.ref_layer_decode.restype = C.c_int
-        R.ref_prefill_loop.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _f32p,
-                                       _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                       C.c_int, C.c_int]
-        R.ref_prefill_loop.restype = C.c_int
-        R.ref_time_decode.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _f32p, _f32p,
-                                      _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                      C.c_int, C.c_int]
-        R.ref_time_decode.restype = C.c_double
-        R.ref_matvec_bf16.argtypes = [_f32p, _u16p, _f32p, C.c_int, C.c_int]
-        R.ref_layer_attention.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, _u16p, C.c_void_p,
-                                          C.c_void_p, _f32p, _f32p, _f32p, C.c_int, C.c_int,
-                                          C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
-        R.ref_layer_attention.restype = C.c_int
-        R.ref_forward_seq.argtypes = [_f32p, _f32p, _i32p, C.c_int, _u16p, C.c_void_p, _u16p,
-                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                                      C.c_int, C.c_int]
-        R.ref_forward_seq.restype = C.c_int
-        R.ref_time_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
-                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
-        R.ref_time_forward.restype = C.c_double
-        _ref = R
+        _ref = _bind_ref(C.CDLL(REF_SO))
     return _ref
+
+
+def _bind_ref(R):
+    """Declares the harness entry points on a loaded reference build."""
+    R.ref_rope_precompute.argtypes = [_f32p, C.c_int, C.c_int, C.c_float]
+    R.ref_rope_apply.argtypes = [_f32p, _f32p, C.c_int, C.c_int]
+    R.ref_rmsnorm_bf16.argtypes = [_f32p, _f32p, _u16p, C.c_int, C.c_float]
+    R.ref_softmax.argtypes = [_f32p, C.c_int]
+    R.ref_causal_mask.argtypes = [_f32p, C.c_int, C.c_int]
+    R.ref_gqa.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                          C.c_float, C.c_void_p, C.c_void_p]
+    R.ref_layer_decode.argtypes = [_f32p, C.c_void_p, C.c_void_p, _f32p, _f32p, _f32p,
+                                   C.c_void_p, C.c_void_p, _f32p, _f32p, _f32p, C.c_int,
+                                   C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+    R.ref_layer_decode.restype = C.c_int
+    R.ref_prefill_loop.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _f32p,
+                                   _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                   C.c_int, C.c_int]
+    R.ref_prefill_loop.restype = C.c_int
+    R.ref_time_decode.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _f32p, _f32p,
+                                  _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                  C.c_int, C.c_int]
+    R.ref_time_decode.restype = C.c_double
+    R.ref_matvec_bf16.argtypes = [_f32p, _u16p, _f32p, C.c_int, C.c_int]
+    R.ref_layer_attention.argtypes = [_f32p, _f32p, _u16p, _u16p, _u16p, _u16p, C.c_void_p,
+                                      C.c_void_p, _f32p, _f32p, _f32p, C.c_int, C.c_int,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+    R.ref_layer_attention.restype = C.c_int
+    R.ref_forward_seq.argtypes = [_f32p, _f32p, _i32p, C.c_int, _u16p, C.c_void_p, _u16p,
+                                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                  C.c_int, C.c_int]
+    R.ref_forward_seq.restype = C.c_int
+    R.ref_time_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                   C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+    R.ref_time_forward.restype = C.c_double
+    return R
 
 
 def _ptr(a):
@@ -412,13 +453,15 @@ def ref_layer_decode(cfg: Config, layer: int, pos: int, q, k, v, k_cache, v_cach
 
 
 def ref_prefill(cfg: Config, layer: int, start_pos: int, Q, K, V, k_cache, v_cache, table,
-                q_norm=None, k_norm=None):
+                q_norm=None, k_norm=None, lib=None):
+    """The reference's prefill loop; lib: a loaded reference build (default
+    ref(); bench.py passes ref_timing())."""
     Q = np.array(Q, dtype=np.float32, copy=True)
     K = np.array(K, dtype=np.float32, copy=True)
     V = np.ascontiguousarray(V, dtype=np.float32)
     n = Q.shape[0]
     out = np.empty((n, cfg.num_heads * cfg.head_dim), dtype=np.float32)
-    rc = ref().ref_prefill_loop(out, Q, K, V, _ptr(q_norm), _ptr(k_norm), k_cache, v_cache, table,
+    rc = (lib or ref()).ref_prefill_loop(out, Q, K, V, _ptr(q_norm), _ptr(k_norm), k_cache, v_cache, table,
                                 cfg.num_heads, cfg.num_kv_heads, layer, start_pos, n,
                                 cfg.max_context, cfg.sliding_window)
     if rc:

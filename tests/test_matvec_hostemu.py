@@ -125,6 +125,25 @@ def test_three_matrices_with_residual_prologue(built, tmp_path, K, post):
         assert err < BAR
 
 
+@pytest.mark.parametrize("K", [100, 12])
+def test_residual_prologue_on_the_scalar_path(built, tmp_path, K):
+    """K a multiple of 4 but not of 8: the residual prologue forms x in LDS
+    and the lane-strided scalar path reads it from there (K = 12: fewer
+    elements than one wave's lanes)."""
+    rng = np.random.default_rng(K + 5)
+    mats = [_bf16(rng, M * K, 0.05).reshape(M, K) for M in (9, 5)]
+    t = rng.standard_normal(K).astype(np.float32)
+    r = (rng.standard_normal(K) * 2).astype(np.float32)
+    wp, wn = _bf16(rng, K, 0.2), _bf16(rng, K, 0.2)
+    ys, r_out = _run(str(tmp_path), mats, K, pre=(t, r, wp, wn))
+    s, x = _prologue_oracle(t, r, wp, wn)
+    assert rel_err(r_out, s) < BAR
+    for y, A in zip(ys, mats):
+        err = rel_err(y, O.matvec_bf16(A, x))
+        print(f"[hostemu matvec prologue scalar] K={K} M={A.shape[0]} rel_err={err:.3e}")
+        assert err < BAR
+
+
 @pytest.mark.parametrize("pre", [False, True])
 def test_geglu(built, tmp_path, pre):
     """gelu_tanh(gate . x) * (up . x), plain and with the residual prologue

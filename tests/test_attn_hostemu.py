@@ -285,16 +285,19 @@ def test_local_prefill_ring(built, tmp_path):
     e.run()
 
 
-def test_key_splits(built, tmp_path):
+@pytest.mark.parametrize("variant", ["default", "qpw32", "fp32"])
+def test_key_splits(built, tmp_path, variant):
     """Global prefills long enough for the host's makespan model to split the
     key tiles of every 64-query block over 2 (n = 256: 4 blocks) and 4
-    (n = 512: 8 blocks) workgroups, with the merge launch (one KV head)."""
+    (n = 512: 8 blocks) workgroups, with the merge launch (one KV head); also
+    with the 32-queries-per-wave kernel and with fp32 values (the V_lo pass)."""
+    env = {"G3ATTN_PREFILL_QPW": 32} if variant == "qpw32" else {}
     for n, splits in [(256, 2), (512, 4)]:
         d = tmp_path / str(n)
         d.mkdir()
         e = Emu(d, H=2, Hkv=1, max_context=640, window=64)
-        e.prefill(5, 0, n)
-        launches = e.run()
+        e.prefill(5, 0, n, bf16=variant != "fp32")
+        launches = e.run(**env)
         assert launches["prefill_kernel"] == (1, n // 64 * splits), launches
         assert launches["prefill_combine_kernel"][0] == 1, launches
 

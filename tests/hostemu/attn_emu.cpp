@@ -32,7 +32,7 @@
 //   prefill_tokens n tokens start logits        (the uploaded model)
 //   destroy
 //
-// At the end it prints "launch <kernel> <launches> <workgroups> <ms>" for every
+// At the end it prints "launch <kernel> <launches> <workgroups> <threads> <ms>" for every
 // kernel launched and "attn_emu: ok".
 #include <cstdio>
 #include <cstdlib>

@@ -482,7 +482,7 @@ template <typename K, typename... A>
 void launch_named(const char *name, K kernel, dim3 grid, dim3 block, A... args) {
     const double t0 = hostemu_now_ms();
     launch(kernel, grid, block, args...);
-    hostemu_count_launch(name, workgroups(grid), hostemu_now_ms() - t0);
+    hostemu_count_launch(name, workgroups(grid), block.x * block.y * block.z, hostemu_now_ms() - t0);
 }
 
 }  // namespace hostemu

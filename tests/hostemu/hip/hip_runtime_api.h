@@ -72,10 +72,11 @@ hipError_t hipEventElapsedTime(float *ms, hipEvent_t start, hipEvent_t stop);
 hipError_t hipGetSymbolAddress(void **p, const void *symbol);
 
 /* Emulator bookkeeping: counts launches, their workgroups and the host
- * milliseconds they took by kernel name (hip_runtime.h's launch macros call
- * it after each launch); hostemu_print_launches writes
- * "launch <name> <launches> <workgroups> <ms>" lines to stdout. */
-void hostemu_count_launch(const char *name, unsigned workgroups, double ms);
+ * milliseconds they took by kernel name, with the last launch's threads per
+ * workgroup (hip_runtime.h's launch macros call it after each launch);
+ * hostemu_print_launches writes
+ * "launch <name> <launches> <workgroups> <threads> <ms>" lines to stdout. */
+void hostemu_count_launch(const char *name, unsigned workgroups, unsigned threads, double ms);
 double hostemu_now_ms(void);
 void hostemu_print_launches(void);
 

@@ -56,6 +56,7 @@ struct LaunchCount {
     int launches = 0;
     unsigned long long workgroups = 0;
     double ms = 0.0;
+    unsigned threads = 0;   // threads per workgroup of the last launch
 };
 std::map<std::string, LaunchCount> &launches() {
     static std::map<std::string, LaunchCount> m;
@@ -176,10 +177,11 @@ hipError_t hipGetSymbolAddress(void **p, const void *symbol) {
     return hipSuccess;
 }
 
-void hostemu_count_launch(const char *name, unsigned workgroups, double ms) {
+void hostemu_count_launch(const char *name, unsigned workgroups, unsigned threads, double ms) {
     LaunchCount &c = launches()[name];
     c.launches++;
     c.workgroups += workgroups;
+    c.threads = threads;
     c.ms += ms;
 }
 
@@ -187,8 +189,8 @@ double hostemu_now_ms(void) { return now_ms(); }
 
 void hostemu_print_launches(void) {
     for (const auto &kv : launches())
-        std::printf("launch %s %d %llu %.1f\n", kv.first.c_str(), kv.second.launches, kv.second.workgroups,
-                    kv.second.ms);
+        std::printf("launch %s %d %llu %u %.1f\n", kv.first.c_str(), kv.second.launches, kv.second.workgroups,
+                    kv.second.threads, kv.second.ms);
 }
 
 }  // extern "C"

@@ -68,6 +68,7 @@ class Emu:
         self.lines = [f"create {H} {Hkv} {max_context} {window} {layers} 1e-6 rl.bin rg.bin {dims}"]
         self.caches = {}
         self.checks = []          # (file, expected, label, bar: x RMS, 0 = exact, or an array bound)
+        self.threads = {}
         self.k = 0
         self.rng = np.random.default_rng(1234)
 
@@ -248,15 +249,17 @@ class Emu:
                 err = rel_err(got, want) if bar else float(np.abs(got - want).max())
             print(f"[hostemu attn] {label}: {err:.3e}")
             assert err <= bar, (label, err)
-        # "launch <kernel expression> <launches> <workgroups> <ms>":
-        # workgroups summed over launches, keyed by the bare kernel name
+        # "launch <kernel expression> <launches> <workgroups> <threads> <ms>":
+        # (launches, workgroups summed over them), keyed by the bare kernel
+        # name; self.threads[name]: threads per workgroup of the last launch
         launches = {}
         for ln in res.stdout.splitlines():
             if ln.startswith("launch "):
-                expr, count, wgs, _ms = ln[len("launch "):].rsplit(" ", 3)
+                expr, count, wgs, threads, _ms = ln[len("launch "):].rsplit(" ", 4)
                 name = expr.strip("()").split("<")[0]
                 c, w = launches.get(name, (0, 0))
                 launches[name] = (c + int(count), w + int(wgs))
+                self.threads[name] = int(threads)
         return launches
 
 
@@ -300,6 +303,7 @@ def test_key_splits(built, tmp_path, variant):
         launches = e.run(**env)
         assert launches["prefill_kernel"] == (1, n // 64 * splits), launches
         assert launches["prefill_combine_kernel"][0] == 1, launches
+        assert e.threads["prefill_kernel"] == (256 if variant == "qpw32" else 512)
 
 
 def test_fp32_values_take_the_v_lo_pass(built, tmp_path):
@@ -330,6 +334,8 @@ def test_prefill_variants(built, tmp_path, env):
     e.prefill(5, 0, 70)
     e.prefill(0, 0, 33)
     e.run(**env)
+    # the 32-query form runs four waves per workgroup, the others eight
+    assert e.threads["prefill_kernel"] == (256 if env.get("G3ATTN_PREFILL_QPW") == 32 else 512)
 
 
 def test_device_entry_and_matmul(built, tmp_path):

@@ -148,6 +148,26 @@ def test_load_forms_agree(monkeypatch):
                 assert np.array_equal(a, b), (n_heads, n_kv, mode)
 
 
+@pytest.mark.parametrize("env", [{"G3ATTN_SPLIT_ROWS": "1000000"}, {"G3ATTN_SPLIT_ROWS": "32"},
+                                 {"G3ATTN_SPLIT_ROWS": "100"}, {"G3ATTN_DECODE_WGS": "8"},
+                                 {"G3ATTN_DECODE_WGS": "4000"}, {"G3ATTN_SPLIT_MIN_ROWS": "512"}])
+def test_split_settings(monkeypatch, env):
+    """The decode's split-shape knobs against the oracle: one split for the
+    whole stream (the kernel writes the normalised output itself), 32-row
+    splits (clamped at the maximum split count for long streams), a length
+    off the 32-row grain, very few and very many workgroups, and a long
+    minimum split.  Local layers in and across the ring wrap and global
+    layers at 3000 and 8191."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    ctx = _ctx(8192, num_layers=6)
+    try:
+        for layer, pos in ((0, 700), (1, 2500), (5, 3000), (5, 8191)):
+            _check(DecodeCase(15, layer=layer, pos=pos, max_context=8192), ctx, ",".join(env.values()))
+    finally:
+        ctx.close()
+
+
 def test_tables_uploaded_after_create():
     """A context created without RoPE tables (the backend hook's init, which
     takes none) refuses attention calls until g3attn_upload_rope, then matches

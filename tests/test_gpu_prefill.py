@@ -213,6 +213,69 @@ def _off_grid(x):
     return (x * np.float32(1.0123457)).astype(np.float32)
 
 
+@pytest.mark.parametrize("layer,start,n,what", [
+    (5, 0, 1500, "all"),          # global: row 0 is v_0 itself, the tightest case
+    (0, 0, 2048, "all"),          # local, full window
+    (11, 300, 400, "hist_v"),     # only the cached values are off the grid
+    (3, 1500, 1200, "batch_v"),   # local ring wrap, only the batch's values
+    (5, 0, 300, "one_v"),         # a single value off the grid sets the flag
+])
+def test_fp32_values(ctx8k, layer, start, n, what):
+    """Values that are not exactly bf16 take the kernel's P_hi.V_lo pass; a
+    bf16-only P.V would miss the bar by ~25x on the early rows here."""
+    case = PrefillCase(50 + layer, layer=layer, start_pos=start, n=n)
+    if what == "all":
+        case.Q, case.K, case.V = _off_grid(case.Q), _off_grid(case.K), _off_grid(case.V)
+        case.v_hist = _off_grid(case.v_hist)
+    elif what == "hist_v":
+        case.v_hist = _off_grid(case.v_hist)
+    elif what == "batch_v":
+        case.V = _off_grid(case.V)
+    else:
+        case.V = case.V.copy()
+        case.V[0, 5] = np.float32(case.V[0, 5] * np.float32(1.0123457))
+    _run(ctx8k, case, f"fp32-{what}")
+
+
+def test_flag_is_per_call(ctx8k):
+    """A call with off-grid values, then a bf16-valued call: each is exact to
+    the bar (the second must not read the first call's stale V_lo rows)."""
+    a = PrefillCase(60, layer=5, start_pos=0, n=700)
+    a.V = _off_grid(a.V)
+    _run(ctx8k, a, "flag-fp32")
+    _run(ctx8k, PrefillCase(61, layer=5, start_pos=0, n=700), "flag-bf16")
+
+
+def test_prefill_then_decode(ctx8k):
+    """Prefill 0..999 then decode at 1000..1004, against the oracle's sequential loop."""
+    cfg = O.Config(max_context=8192)
+    for layer in (5, 0):
+        case = PrefillCase(38, layer=layer, start_pos=0, n=1000)
+        case.gpu(ctx8k)
+        _, Kc, Vc = case.oracle()
+        zn = O.zero_norm()
+        for pos in range(1000, 1005):
+            q = O.gen_normal_bf16(2048, 0xD00 + pos)
+            k = O.gen_normal_bf16(1024, 0xE00 + pos)
+            v = O.gen_normal_bf16(1024, 0xF00 + pos)
+            want, _, _ = O.layer_decode(cfg, layer, pos, q, k, v, Kc, Vc, case.table, zn, zn)
+            got = ctx8k.decode(layer, pos, q, k, v, zn, zn)
+            assert rel_err(got, want) < 1e-4, (layer, pos)
+
+
+def test_prefill_errors(ctx8k):
+    Q = np.zeros((4, 2048), np.float32)
+    K = np.zeros((4, 1024), np.float32)
+    with pytest.raises(G.G3AttnError) as e:
+        ctx8k.prefill(5, 8190, Q, K, K)
+    assert e.value.rc == G.ERR_CONTEXT_OVERFLOW
+    with pytest.raises(G.G3AttnError) as e:
+        ctx8k.prefill(34, 0, Q, K, K)
+    assert e.value.rc == G.ERR_INVALID_ARG
+    out = ctx8k.prefill(5, 0, Q[:0], K[:0], K[:0])
+    assert out.shape == (0, 2048)
+
+
 def _forms_cases():
     """(context kwargs, [(label, case)]) for the selectable-forms test."""
     big = []

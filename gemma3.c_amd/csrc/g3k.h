@@ -154,11 +154,19 @@ typedef struct {
     /* Key splits (1, 2 or 4).  With S > 1 every (query block, KV head) runs as
      * S workgroups over consecutive parts of its key tiles; each writes its
      * unnormalised O and (max, sum) per query row to part_o [S][n][H_q][D]
-     * and part_ml [S][n][H_q][2], and a second launch merges the S parts
-     * into out (in split order: deterministic). */
+     * and part_ml [S][n][H_q][2], then counts itself in arrive[qb * H_kv +
+     * kvh] (an atomic increment that wraps to 0 after S arrivals, so the
+     * counters start every call at zero).  The last of the S workgroups to
+     * arrive merges the S parts into out, in split order (deterministic).
+     * arrive holds G3K_PREFILL_ARRIVE(max_n, H_kv) zeroed counters. */
     int ksplit;
     float *part_o, *part_ml;
+    unsigned *arrive;
 } g3k_prefill_args;
+
+/* arrival counters a prefill of up to n tokens can index: query blocks of at
+ * least 32 positions, one counter per (query block, KV head) */
+#define G3K_PREFILL_ARRIVE(n, n_kv) ((((n) + 31) / 32) * (n_kv))
 
 int g3k_prefill(const g3k_prefill_args *a, void *stream);
 

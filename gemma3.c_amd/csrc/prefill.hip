@@ -74,6 +74,11 @@ constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Cache-policy bits of a buffer access: sc1, agent-coherent (written through
+// to / read from the point of coherence shared by every XCD).
+constexpr int CP_SC1 = 16;
 
 __device__ __forceinline__ uint16_t f16_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ uint16_t bf16_bits(__bf16 h) { return __builtin_bit_cast(uint16_t, h); }
@@ -547,25 +552,101 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         __syncthreads();
     }
 
-    // ---- normalise and write attn_out[token][qhead][dim], or this split's
-    // unnormalised part ----
-    if (!wave_live) return;
+    // ---- normalise and write attn_out[token][qhead][dim]; with key splits,
+    // publish this split's unnormalised part and let the last split of the
+    // block to arrive merge them ----
     if (S > 1) {
         const int hq = p.n_kv_heads * G;
+        // Parts are written and read with agent-coherent (sc1) accesses,
+        // which go to and come from the point of coherence shared by all
+        // XCDs, so no cache-wide writeback or invalidate is needed.  (An
+        // agent-scope __threadfence does both to the XCD's whole L2; with
+        // one per workgroup configs[2] took 188 us instead of 53.)  The
+        // parts of split s of this block are one run of PB * H_q rows: one
+        // descriptor per split, offsets relative to the block's first token.
+        auto part_rsrc = [&](int sp) {
+            return make_rsrc(p.part_o + ((size_t)sp * p.n + (size_t)qb * PB) * hq * D, (unsigned)(PB * hq * D * 4));
+        };
+        float lt[NQB];
 #pragma unroll
         for (int b = 0; b < NQB; b++) {
-            const float lt = col4_sum(l_sum[b]);   // all lanes active here
+            lt[b] = col4_sum(l_sum[b]);   // all lanes active here
             const int tok = tok0 + 16 * b + ln;
-            if (tok >= p.n) continue;
-            const size_t row = ((size_t)split * p.n + tok) * hq + qhead;
-            float *po = p.part_o + row * D + 4 * g;
+            if (!wave_live || tok >= p.n) continue;
+            const __amdgpu_buffer_rsrc_t pr = part_rsrc(split);
+            const unsigned voff = (unsigned)((((tok - qb * PB) * hq + qhead) * D + 4 * g) * 4);
 #pragma unroll
             for (int mt = 0; mt < 16; mt++)
-                *reinterpret_cast<float4 *>(po + 16 * mt) = make_float4(o[b][mt][0], o[b][mt][1], o[b][mt][2], o[b][mt][3]);
-            if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + row * 2) = make_float2(m_ref[b], lt);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[b][mt]), pr, voff + 64 * mt, 0, CP_SC1);
+            if (g == 0) {
+                float *ml = p.part_ml + (((size_t)split * p.n + tok) * hq + qhead) * 2;
+                __hip_atomic_store(ml, m_ref[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(ml + 1, lt[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        // Every part store of the wave has completed (vmcnt counts stores on
+        // this family) before the block's arrival is counted; the counter
+        // wraps to 0 on the S-th arrival, ready for the next call.  The
+        // loop's last barrier has retired every LDS access, so the flag
+        // reuses smem.
+        G3K_WAIT_VMEM();
+        __syncthreads();
+        int *last = reinterpret_cast<int *>(smem);
+        if (tid == 0) *last = atomicInc(p.arrive + (size_t)qb * p.n_kv_heads + kvh, (unsigned)(S - 1)) == (unsigned)(S - 1);
+        __syncthreads();
+        if (!*last || !wave_live) return;
+        // merge in split order, as out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s;
+        // this split's part is still in registers
+#pragma unroll
+        for (int b = 0; b < NQB; b++) {
+            const int tok = tok0 + 16 * b + ln;
+            if (tok >= p.n) continue;
+            const unsigned voff = (unsigned)((((tok - qb * PB) * hq + qhead) * D + 4 * g) * 4);
+            // S <= 4: fixed trip counts keep ms / ls in registers
+            float ms[4], ls[4];
+            float M = NEG_BIG;
+#pragma unroll
+            for (int sp = 0; sp < 4; sp++) {
+                if (sp >= S) break;
+                if (sp == split) {
+                    ms[sp] = m_ref[b];
+                    ls[sp] = lt[b];
+                } else {
+                    const float *ml = p.part_ml + (((size_t)sp * p.n + tok) * hq + qhead) * 2;
+                    ms[sp] = __hip_atomic_load(ml, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ls[sp] = __hip_atomic_load(ml + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                M = fmaxf(M, ms[sp]);
+            }
+            float L = 0.f;
+            f32x4 A[16];
+#pragma unroll
+            for (int mt = 0; mt < 16; mt++) A[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sp = 0; sp < 4; sp++) {
+                if (sp >= S) break;
+                const float f = fast_exp2(ms[sp] - M);
+                L += ls[sp] * f;
+                if (sp == split) {
+#pragma unroll
+                    for (int mt = 0; mt < 16; mt++) A[mt] += o[b][mt] * f;
+                } else {
+                    const __amdgpu_buffer_rsrc_t pr = part_rsrc(sp);
+#pragma unroll
+                    for (int mt = 0; mt < 16; mt++)
+                        A[mt] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, voff + 64 * mt, 0, CP_SC1)) * f;
+                }
+            }
+            const float inv = 1.0f / L;
+            float *orow = p.out + ((size_t)tok * hq + qhead) * D + 4 * g;
+#pragma unroll
+            for (int mt = 0; mt < 16; mt++)
+                *reinterpret_cast<float4 *>(orow + 16 * mt) =
+                    make_float4(A[mt][0] * inv, A[mt][1] * inv, A[mt][2] * inv, A[mt][3] * inv);
         }
         return;
     }
+    if (!wave_live) return;
 #pragma unroll
     for (int b = 0; b < NQB; b++) {
         const float inv = 1.0f / col4_sum(l_sum[b]);   // all lanes active here
@@ -590,29 +671,6 @@ __global__ __launch_bounds__(512 / NQB, 1) void prefill_kernel(g3k_prefill_args 
         attend<G, NQB, false>(p, smem);
 }
 
-// Merge of the key splits' parts for one (token, query head) row: one wave,
-// lane t owns dims 4t .. 4t + 3; out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
-__global__ __launch_bounds__(64) void prefill_combine_kernel(g3k_prefill_args p) {
-    const size_t row = blockIdx.x, rows = (size_t)p.n * p.n_kv_heads * p.group;
-    const int t = threadIdx.x;
-    float M = NEG_BIG;
-    for (int s = 0; s < p.ksplit; s++) M = fmaxf(M, p.part_ml[(s * rows + row) * 2]);
-    float L = 0.f;
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < p.ksplit; s++) {
-        const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (s * rows + row) * 2);
-        const float f = fast_exp2(ml.x - M);
-        const float4 o = *reinterpret_cast<const float4 *>(p.part_o + (s * rows + row) * D + 4 * t);
-        L += ml.y * f;
-        A.x += o.x * f;
-        A.y += o.y * f;
-        A.z += o.z * f;
-        A.w += o.w * f;
-    }
-    const float inv = 1.0f / L;
-    *reinterpret_cast<float4 *>(p.out + row * D + 4 * t) = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
-}
-
 template <int G, int NQB>
 hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
     constexpr int PB = 16 * NQB * ((8 / NQB) / G);
@@ -620,9 +678,6 @@ hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
     // With timing events the dispatch itself records them (kernel begin / end).
     hipExtLaunchKernelGGL((prefill_kernel<G, NQB>), dim3(nqb * a->n_kv_heads * a->ksplit), dim3(512 / NQB), 0,
                           st, (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a->ksplit == 1) return e;
-    hipLaunchKernelGGL(prefill_combine_kernel, dim3(a->n * a->n_kv_heads * G), dim3(D / 4), 0, st, *a);
     return hipGetLastError();
 }
 
@@ -643,7 +698,8 @@ extern "C" int g3k_prefill(const g3k_prefill_args *a, void *stream) {
     if (a->ldk % 64 || a->ldk > (1LL << 20) || a->nk > a->ldk || a->hist + a->n != a->nk ||
         a->window < 1 || !a->v_lo_flag)
         return (int)hipErrorInvalidValue;
-    if ((a->ksplit != 1 && a->ksplit != 2 && a->ksplit != 4) || (a->ksplit > 1 && (!a->part_o || !a->part_ml)))
+    if ((a->ksplit != 1 && a->ksplit != 2 && a->ksplit != 4) ||
+        (a->ksplit > 1 && (!a->part_o || !a->part_ml || !a->arrive)))
         return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const bool wide = a->queries_per_wave == 32;

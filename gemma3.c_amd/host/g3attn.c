@@ -132,6 +132,9 @@ struct g3attn_ctx {
      * bf16 (the attention kernel then adds its V_lo pass) */
     int *d_vflag;
     int pf_epoch;
+    /* prefill key splits: per (query block, KV head) arrival counters, zeroed
+     * once; each call's S arrivals wrap them back to zero */
+    unsigned *d_arrive;
     /* kernel timing (g3attn_profile_*): event pairs per kind */
     struct {
         int on;
@@ -186,6 +189,7 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_big);
     hipFree(c->d_pf);
     hipFree(c->d_vflag);
+    hipFree(c->d_arrive);
     hipFree(c->d_la);
     hipFree(c->d_fw);
     hipFree(c->d_wt);
@@ -301,6 +305,11 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
     if (!alloc_dev((void **)&c->ws_ml, slots * 2 * sizeof(float), "decode workspace")) goto fail;
     if (!alloc_dev((void **)&c->d_vflag, sizeof(int), "prefill flag")) goto fail;
     if (hipMemset(c->d_vflag, 0, sizeof(int)) != hipSuccess) goto fail_rt;
+    {
+        const size_t nb = (size_t)G3K_PREFILL_ARRIVE(max_context, cfg->num_kv_heads) * sizeof(unsigned);
+        if (!alloc_dev((void **)&c->d_arrive, nb, "prefill arrival counters")) goto fail;
+        if (hipMemset(c->d_arrive, 0, nb) != hipSuccess) goto fail_rt;
+    }
     {
         const char *w = getenv("G3ATTN_DECODE_WGS");
         const char *mr = getenv("G3ATTN_SPLIT_MIN_ROWS");
@@ -766,15 +775,16 @@ static int grow_pf(g3attn_ctx *c, size_t bytes) {
 
 /* Key splits S (1, 2 or 4) of a prefill call.  A workgroup walks the key
  * tiles of one query block (pb tokens) of one KV head; with S > 1 each
- * block's tiles are dealt to S workgroups and a second launch merges their
- * parts.  S minimises a makespan model measured on MI355X:
+ * block's tiles are dealt to S workgroups, and the last of them to finish
+ * merges their parts (inside the kernel).  S minimises a makespan model
+ * measured on MI355X:
  * - a tile step costs ~2.2 us, and a workgroup ~12 us more: its prologue
  *   (queries, RoPE rows and the first K / V tiles, read while every CU does
  *   the same) and its output stores;
  * - one workgroup runs per CU (its LDS), and the longest block's part sets a
  *   floor (a 4096-token global prefill unsplit: 128 tiles on one CU while
  *   the average is 65);
- * - the merge moves (S + 1) n H_q 256 floats at ~5 TB/s, plus a launch.
+ * - the parts and the merge move about (S + 1) n H_q 256 floats at ~5 TB/s.
  * Each split keeps at least 4 tiles. */
 static int prefill_splits(int n, int hist, int nk, int window, int pb, int n_kv, int n_q, int n_cu) {
     const int nb = (n + pb - 1) / pb;
@@ -952,6 +962,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.ksplit = S;
     pa.part_o = part_o;
     pa.part_ml = part_ml;
+    pa.arrive = c->d_arrive;
     rc = prof_slot(c, 1, &pa.ev0, &pa.ev1);
     if (rc) return rc;
     rc = g3k_prefill(&pa, c->stream);

@@ -7,8 +7,9 @@
 // This header supplies the subset of the HIP device language those kernels
 // use, emulated on the host (the runtime API is hip_runtime_api.h):
 //
-//   - A launch runs every workgroup of the grid in turn on one team of
-//     blockDim fibers (one stack per GPU thread, all on the calling OS
+//   - A launch runs every workgroup of the grid in turn (first to last, or
+//     last to first with HOSTEMU_WG_ORDER=reverse) on one team of blockDim
+//     fibers (one stack per GPU thread, all on the calling OS
 //     thread), so 64 consecutive fibers form one wave64.  __shared__ becomes
 //     a function-local static: one copy, used by one workgroup at a time.
 //   - __syncthreads is a barrier over the team; every cross-lane operation
@@ -207,6 +208,20 @@ inline int __syncthreads_or(int p) {
     m.block.wait();   // every thread has read the slots before any rewrites them
     return r;
 }
+// Workgroups run one after another, so a fence has nothing to order and an
+// atomic is a plain read-modify-write.  atomicInc wraps as the hardware's
+// atomic_inc does: old >= v ? 0 : old + 1.
+inline void __threadfence() {}
+// (__hip_atomic_load / __hip_atomic_store are clang builtins on the host
+// too; only their scope names are HIP-mode macros.)
+#ifndef __HIP_MEMORY_SCOPE_AGENT
+#define __HIP_MEMORY_SCOPE_AGENT 4
+#endif
+inline unsigned atomicInc(unsigned *p, unsigned v) {
+    const unsigned old = *p;
+    *p = old >= v ? 0u : old + 1u;
+    return old;
+}
 
 // ---- cross-lane builtins ---------------------------------------------------------
 // DPP (row = 16 lanes): quad_perm 0x00-0xff, row_ror:8 0x128 (lane i reads
@@ -295,8 +310,18 @@ inline std::array<uint32_t, 4> hostemu_raw_buffer_load_b128(__amdgpu_buffer_rsrc
     std::memcpy(v.data(), r.base + off, 16);
     return v;
 }
+// 16-byte buffer store; out of range aborts (the hardware would drop it).
+template <typename T>
+inline void hostemu_raw_buffer_store_b128(T v, __amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, int aux) {
+    static_assert(sizeof(T) == 16, "b128 store");
+    (void)aux;
+    const uint64_t off = (uint64_t)voff + soff;
+    if (off + 16 > r.num_records) hostemu::fail("buffer store beyond num_records");
+    std::memcpy(const_cast<char *>(r.base) + off, &v, 16);
+}
 #define __builtin_amdgcn_make_buffer_rsrc hostemu_make_buffer_rsrc
 #define __builtin_amdgcn_raw_buffer_load_b128 hostemu_raw_buffer_load_b128
+#define __builtin_amdgcn_raw_buffer_store_b128 hostemu_raw_buffer_store_b128
 
 // Buffer -> LDS load (gfx950 buffer_load_dwordx4 ... lds), 16 bytes per lane:
 // lane l's 16 bytes go to LDS at the given base + 16 l.  A dword whose
@@ -423,14 +448,19 @@ void launch(K kernel, dim3 grid, dim3 block, A... args) {
     m.waves = std::vector<Wave>(nt / 64);
     m.slot = std::vector<int>(nt);
     for (auto &w : m.waves) w.bar.n = 64;
+    // HOSTEMU_WG_ORDER=reverse runs the workgroups last to first, so a
+    // result that depends on which workgroup of a group arrives last (the
+    // prefill key-split merge) is checked in both orders.
+    const char *order = std::getenv("HOSTEMU_WG_ORDER");
+    const bool reverse = order && !std::strcmp(order, "reverse");
     m.body = [&] {
-        for (unsigned z = 0; z < grid.z; z++)
-            for (unsigned y = 0; y < grid.y; y++)
-                for (unsigned x = 0; x < grid.x; x++) {
-                    blockIdx = dim3(x, y, z);
-                    kernel(args...);
-                    __syncthreads();  // the workgroup has ended before the next one starts
-                }
+        const unsigned nwg = grid.x * grid.y * grid.z;
+        for (unsigned i = 0; i < nwg; i++) {
+            const unsigned w = reverse ? nwg - 1 - i : i;
+            blockIdx = dim3(w % grid.x, (w / grid.x) % grid.y, w / (grid.x * grid.y));
+            kernel(args...);
+            __syncthreads();  // the workgroup has ended before the next one starts
+        }
     };
     const size_t stack_size = (size_t)1 << 17;
     for (int i = 0; i < nt; i++) {

@@ -288,21 +288,32 @@ def test_local_prefill_ring(built, tmp_path):
     e.run()
 
 
+@pytest.mark.parametrize("order", ["forward", "reverse"])
 @pytest.mark.parametrize("variant", ["default", "qpw32", "fp32"])
-def test_key_splits(built, tmp_path, variant):
+def test_key_splits(built, tmp_path, variant, order):
     """Global prefills long enough for the host's makespan model to split the
     key tiles of every 64-query block over 2 (n = 256: 4 blocks) and 4
-    (n = 512: 8 blocks) workgroups, with the merge launch (one KV head); also
-    with the 32-queries-per-wave kernel and with fp32 values (the V_lo pass)."""
+    (n = 512: 8 blocks) workgroups (one KV head), merged inside the kernel
+    by the split that arrives last: the last split of each block when the
+    workgroups run in grid order, split 0 when they run in reverse.  Also
+    with the 32-queries-per-wave kernel and with fp32 values (the V_lo pass).
+    The prefill is followed by decodes over the same cache, so the arrival
+    counters are reused by a second prefill of the same context."""
     env = {"G3ATTN_PREFILL_QPW": 32} if variant == "qpw32" else {}
+    if order == "reverse":
+        env["HOSTEMU_WG_ORDER"] = "reverse"
     for n, splits in [(256, 2), (512, 4)]:
         d = tmp_path / str(n)
         d.mkdir()
         e = Emu(d, H=2, Hkv=1, max_context=640, window=64)
         e.prefill(5, 0, n, bf16=variant != "fp32")
+        e.prefill(5, n, 64, bf16=variant != "fp32")
         launches = e.run(**env)
-        assert launches["prefill_kernel"] == (1, n // 64 * splits), launches
-        assert launches["prefill_combine_kernel"][0] == 1, launches
+        # (launches, workgroups over both calls): the first call alone has
+        # n / 64 blocks x `splits`, the 64-token second call at least one
+        assert launches["prefill_kernel"][0] == 2, launches
+        assert launches["prefill_kernel"][1] > n // 64 * splits, launches
+        assert "prefill_combine_kernel" not in launches, launches
         assert e.threads["prefill_kernel"] == (256 if variant == "qpw32" else 512)
 
 

@@ -124,6 +124,11 @@ typedef struct {
 
 int g3k_stage(const g3k_stage_args *a, void *stream);
 
+/* g3k_rope_write (without queries: ra->Q == NULL) and g3k_stage in one
+ * launch, for a batch whose staging reads only the batch's own inputs (not
+ * the cache rows the same batch writes). */
+int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_stage_args *sa, void *stream);
+
 /* Causal / sliding-window prefill attention on MFMA (one launch).
  *   q:  raw (pre-norm) queries [n][n_heads][D] fp32, the reference's Q_all
  *       layout; the kernel applies QK-norm (q_norm, NULL = none) and RoPE

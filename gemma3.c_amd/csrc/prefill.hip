@@ -52,6 +52,7 @@
 
 #include "g3k.h"
 #include "g3k_device.h"
+#include "rope_write_body.h"
 
 namespace {
 
@@ -88,9 +89,8 @@ __device__ __forceinline__ uint16_t bf16_bits(__bf16 h) { return __builtin_bit_c
 // V^T columns.  Workgroup = 64 keys x 64 dims of one head (grid: key blocks,
 // D/64, H_kv).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) {
+__device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int dx, int h) {
     __shared__ uint16_t s_t[2][64][64 + 8];
-    const int kb = blockIdx.x, dx = blockIdx.y, h = blockIdx.z;
     const int tid = threadIdx.x;
     const int kkbase = a.kk0 + kb * 64;
     const int kend = a.kk0 + a.cnt;
@@ -158,6 +158,23 @@ __global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) {
             for (int e = 0; kk + e < kend; e++) dst[e] = s[e];
         }
     }
+}
+
+__global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) { stage_block(a, blockIdx.x, blockIdx.y, blockIdx.z); }
+
+// The batch's front end in one launch: the V^T staging blocks of `sa` (first:
+// fewer and heavier) and the waves of rope_write_vec over `ra` (K-norm,
+// RoPE, cache write, fp16 hi | lo key rows).  The two read the batch's K / V
+// inputs and write disjoint buffers, so their order does not matter.
+__global__ __launch_bounds__(NT) void front_kernel(g3k_rope_write_args ra, g3k_stage_args sa, unsigned stage_blocks,
+                                                   unsigned kblocks) {
+    const unsigned b = blockIdx.x;
+    if (b < stage_blocks) {
+        const unsigned per_head = kblocks * (D / 64);
+        stage_block(sa, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head));
+        return;
+    }
+    rope_write_vec(ra, ((long long)(b - stage_blocks) * NT + threadIdx.x) >> 6, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------
@@ -688,6 +705,19 @@ extern "C" int g3k_stage(const g3k_stage_args *a, void *stream) {
     if (a->ldk % 64 || a->kk0 + a->cnt > a->ldk || !a->v_lo_flag) return (int)hipErrorInvalidValue;
     dim3 grid((a->cnt + 63) / 64, D / 64, a->n_kv_heads);
     hipLaunchKernelGGL(stage_kernel, grid, dim3(NT), 0, (hipStream_t)stream, *a);
+    return (int)hipGetLastError();
+}
+
+extern "C" int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_stage_args *sa, void *stream) {
+    if (ra->n <= 0 && sa->cnt <= 0) return 0;
+    if (sa->cnt > 0 && (sa->ldk % 64 || sa->kk0 + sa->cnt > sa->ldk || !sa->v_lo_flag)) return (int)hipErrorInvalidValue;
+    if (ra->n > 0 && ra->Q) return (int)hipErrorInvalidValue;   // the prefill front end stages no queries
+    const long long kblocks = sa->cnt > 0 ? (sa->cnt + 63) / 64 : 0;
+    const long long stage_blocks = kblocks * (D / 64) * sa->n_kv_heads;
+    const long long rw_blocks = ra->n > 0 ? ((long long)ra->n * 2 * ra->n_kv_heads + 3) / 4 : 0;
+    if (stage_blocks + rw_blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(front_kernel, dim3((unsigned)(stage_blocks + rw_blocks)), dim3(NT), 0, (hipStream_t)stream, *ra,
+                       *sa, (unsigned)stage_blocks, (unsigned)kblocks);
     return (int)hipGetLastError();
 }
 

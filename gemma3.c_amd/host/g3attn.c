@@ -908,9 +908,8 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     ra.kq = kq;
     ra.ldk = ldk;
     ra.row0 = hist;
-    rc = g3k_rope_write(&ra, c->stream);
-    if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill rope");
-    /* 3. the batch's values as bf16 hi / lo V^T, and zeroed padding up to ldk */
+    /* 3. the batch's values as bf16 hi / lo V^T, and zeroed padding up to
+     *    ldk: read from the batch's own V, so it runs in step 2's launch */
     {
         g3k_stage_args sa;
         memset(&sa, 0, sizeof sa);
@@ -931,8 +930,8 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
         sa.ldk = ldk;
         sa.v_lo_flag = c->d_vflag;
         sa.epoch = c->pf_epoch;
-        rc = g3k_stage(&sa, c->stream);
-        if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill stage");
+        rc = g3k_rope_write_stage(&ra, &sa, c->stream);
+        if (rc) return hip_fail((hipError_t)rc, "g3attn_prefill rope / stage");
     }
     /* 4. Q-norm + RoPE and attention (gemma3_transformer.c:650-667 for the
      *    queries, gemma3_gqa for every token, :673-691) */

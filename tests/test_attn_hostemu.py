@@ -273,7 +273,11 @@ def test_global_prefill_chunks_then_decode(built, tmp_path):
     e.decode(5, 71)
     e.check_cache(5, 0, 72)
     launches = e.run()
-    assert launches["stage_kernel"][0] == 3   # the batch's values x 2, the history once
+    # the history is staged once by its own launch; each chunk's values are
+    # staged inside that chunk's front launch (with K-norm, RoPE, cache write)
+    assert launches["stage_kernel"][0] == 1, launches
+    assert launches["front_kernel"][0] == 2, launches
+    assert "rope_write_kernel" not in launches, launches
 
 
 def test_local_prefill_ring(built, tmp_path):

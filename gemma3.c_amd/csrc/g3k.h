@@ -124,9 +124,10 @@ typedef struct {
 
 int g3k_stage(const g3k_stage_args *a, void *stream);
 
-/* g3k_rope_write (without queries: ra->Q == NULL) and g3k_stage in one
- * launch, for a batch whose staging reads only the batch's own inputs (not
- * the cache rows the same batch writes). */
+/* g3k_rope_write (without queries: ra->Q == NULL) and g3k_stage of the same
+ * batch's values (sa: V only, from ra->V, key indices from the batch's first
+ * token on) in one launch; the staging blocks also write the batch's V rows
+ * to the cache, so V is read once. */
 int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_stage_args *sa, void *stream);
 
 /* Causal / sliding-window prefill attention on MFMA (one launch).

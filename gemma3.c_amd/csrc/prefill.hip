@@ -89,7 +89,11 @@ __device__ __forceinline__ uint16_t bf16_bits(__bf16 h) { return __builtin_bit_c
 // V^T columns.  Workgroup = 64 keys x 64 dims of one head (grid: key blocks,
 // D/64, H_kv).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int dx, int h) {
+// vc != nullptr (the prefill front launch, staging the batch's own V): the
+// staged V values are also written to the cache rows vc describes
+// (rope_write_vec's destination rules), so the batch's V is read once.
+__device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int dx, int h,
+                                            const g3k_rope_write_args *vc = nullptr) {
     __shared__ uint16_t s_t[2][64][64 + 8];
     const int tid = threadIdx.x;
     const int kkbase = a.kk0 + kb * 64;
@@ -109,6 +113,11 @@ __device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int
             const size_t off = (size_t)h * a.head_stride + (size_t)row * a.row_stride + dx * 64 + col;
             vv = *reinterpret_cast<const float4 *>(a.v_src + off);
             if (a.k_src) kv = *reinterpret_cast<const float4 *>(a.k_src + off);
+            if (vc && pos - vc->start_pos >= vc->kv_skip) {
+                const int slot = vc->ring > 0 ? pos % vc->ring : pos - vc->dst_pos0;
+                *reinterpret_cast<float4 *>(vc->v_dst + (size_t)h * vc->dst_head_stride + (size_t)slot * D + dx * 64 +
+                                            col) = vv;
+            }
         }
         if (a.k_src || kk >= a.nk) {
             const float x[4] = {kv.x, kv.y, kv.z, kv.w};
@@ -163,18 +172,23 @@ __device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int
 __global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) { stage_block(a, blockIdx.x, blockIdx.y, blockIdx.z); }
 
 // The batch's front end in one launch: the V^T staging blocks of `sa` (first:
-// fewer and heavier) and the waves of rope_write_vec over `ra` (K-norm,
-// RoPE, cache write, fp16 hi | lo key rows).  The two read the batch's K / V
-// inputs and write disjoint buffers, so their order does not matter.
+// fewer and heavier), which also write the batch's V rows to the cache, and
+// the K waves of rope_write_vec over `ra` (K-norm, RoPE, cache write, fp16
+// hi | lo key rows).  The two read disjoint inputs (V / K) and write
+// disjoint buffers, so their order does not matter.
 __global__ __launch_bounds__(NT) void front_kernel(g3k_rope_write_args ra, g3k_stage_args sa, unsigned stage_blocks,
                                                    unsigned kblocks) {
     const unsigned b = blockIdx.x;
     if (b < stage_blocks) {
         const unsigned per_head = kblocks * (D / 64);
-        stage_block(sa, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head));
+        stage_block(sa, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head), &ra);
         return;
     }
-    rope_write_vec(ra, ((long long)(b - stage_blocks) * NT + threadIdx.x) >> 6, threadIdx.x & 63);
+    // K wave kw = token i x H_kv + head h is rope_write_vec's vector i x
+    // (2 H_kv) + h (no queries: K heads first, then V heads)
+    const long long kw = ((long long)(b - stage_blocks) * NT + threadIdx.x) >> 6;
+    const long long i = kw / ra.n_kv_heads, h = kw % ra.n_kv_heads;
+    rope_write_vec(ra, i < ra.n ? i * (2 * ra.n_kv_heads) + h : (long long)ra.n * 2 * ra.n_kv_heads, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------------------
@@ -714,7 +728,13 @@ extern "C" int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_sta
     if (ra->n > 0 && ra->Q) return (int)hipErrorInvalidValue;   // the prefill front end stages no queries
     const long long kblocks = sa->cnt > 0 ? (sa->cnt + 63) / 64 : 0;
     const long long stage_blocks = kblocks * (D / 64) * sa->n_kv_heads;
-    const long long rw_blocks = ra->n > 0 ? ((long long)ra->n * 2 * ra->n_kv_heads + 3) / 4 : 0;
+    // the staging blocks write the batch's V rows to the cache: they must
+    // cover every token of ra (key indices kk0 .. kk0 + n - 1, positions
+    // start_pos ..) and read V from the batch's own rows
+    if (ra->n > 0 && (sa->cnt < ra->n || sa->k_src || sa->ring || sa->row_pos0 != ra->start_pos ||
+                      sa->kstart + sa->kk0 != ra->start_pos || sa->v_src != ra->V || sa->n_kv_heads != ra->n_kv_heads))
+        return (int)hipErrorInvalidValue;
+    const long long rw_blocks = ra->n > 0 ? ((long long)ra->n * ra->n_kv_heads + 3) / 4 : 0;
     if (stage_blocks + rw_blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(front_kernel, dim3((unsigned)(stage_blocks + rw_blocks)), dim3(NT), 0, (hipStream_t)stream, *ra,
                        *sa, (unsigned)stage_blocks, (unsigned)kblocks);

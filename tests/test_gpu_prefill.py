@@ -318,3 +318,26 @@ def test_selectable_prefill_forms(monkeypatch, env):
                 assert np.array_equal(got, same), (label, name)
         for k in env:
             monkeypatch.delenv(k)
+
+
+def test_split_merge_repeats_in_one_context(ctx8k):
+    """Key-split prefills merge inside the kernel: the last split of each
+    block to arrive (whichever it is on a given run) merges the parts in split
+    order, and the per-block arrival counters wrap back to zero after every
+    call.  Alternating a 2-split local prefill (configs[2]'s shape) and a
+    4-split 2048-token global prefill three times in one context reuses the
+    counters with a changing split count; every repeat matches the first bit
+    for bit, and the first matches the oracle."""
+    cases = [PrefillCase(70, layer=2, start_pos=0, n=2048), PrefillCase(71, layer=5, start_pos=0, n=2048)]
+    first = []
+    for rep in range(3):
+        for i, case in enumerate(cases):
+            got = case.gpu(ctx8k)
+            if rep == 0:
+                want, _, _ = case.oracle()
+                err = rel_err(got, want)
+                print(f"[split merge case {i}] rel_err={err:.3e}", flush=True)
+                assert err <= TOL, (i, err)
+                first.append(got)
+            else:
+                assert np.array_equal(got, first[i]), (rep, i)

@@ -761,7 +761,7 @@ def main():
                         "8 Q / 4 KV heads, head_dim 256, fp32 KV cache",
             "us_per_token": None if ms_per_step is None else round(ms_per_step * 1e3, 3),
             "bytes_per_step": decode_bytes(8192),
-            "llc": "10 distinct 64 MiB caches rotated (640 MiB > 256 MB Infinity Cache)",
+            "llc": "each timed region rotates 5 distinct 64 MiB caches (320 MiB > 256 MB Infinity Cache); two such contexts are timed in turn and averaged",
         },
         "roofline": None if achieved is None else {
             "bound": "hbm",

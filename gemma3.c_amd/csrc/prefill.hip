@@ -113,7 +113,7 @@ __device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int
             const size_t off = (size_t)h * a.head_stride + (size_t)row * a.row_stride + dx * 64 + col;
             vv = *reinterpret_cast<const float4 *>(a.v_src + off);
             if (a.k_src) kv = *reinterpret_cast<const float4 *>(a.k_src + off);
-            if (vc && pos - vc->start_pos >= vc->kv_skip) {
+            if (vc && pos - vc->start_pos >= vc->kv_skip && pos - vc->start_pos < vc->n) {
                 const int slot = vc->ring > 0 ? pos % vc->ring : pos - vc->dst_pos0;
                 *reinterpret_cast<float4 *>(vc->v_dst + (size_t)h * vc->dst_head_stride + (size_t)slot * D + dx * 64 +
                                             col) = vv;
@@ -181,7 +181,9 @@ __global__ __launch_bounds__(NT) void front_kernel(g3k_rope_write_args ra, g3k_s
     const unsigned b = blockIdx.x;
     if (b < stage_blocks) {
         const unsigned per_head = kblocks * (D / 64);
-        stage_block(sa, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head), &ra);
+        // the cache rows are written only for a batch that has tokens
+        stage_block(sa, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head),
+                    ra.n > 0 ? &ra : nullptr);
         return;
     }
     // K wave kw = token i x H_kv + head h is rope_write_vec's vector i x
@@ -731,7 +733,8 @@ extern "C" int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_sta
     // the staging blocks write the batch's V rows to the cache: they must
     // cover every token of ra (key indices kk0 .. kk0 + n - 1, positions
     // start_pos ..) and read V from the batch's own rows
-    if (ra->n > 0 && (sa->cnt < ra->n || sa->k_src || sa->ring || sa->row_pos0 != ra->start_pos ||
+    if (ra->n > 0 && (sa->cnt < ra->n || sa->nk != sa->kk0 + ra->n || sa->k_src || sa->ring ||
+                      sa->row_pos0 != ra->start_pos ||
                       sa->kstart + sa->kk0 != ra->start_pos || sa->v_src != ra->V || sa->n_kv_heads != ra->n_kv_heads))
         return (int)hipErrorInvalidValue;
     const long long rw_blocks = ra->n > 0 ? ((long long)ra->n * ra->n_kv_heads + 3) / 4 : 0;

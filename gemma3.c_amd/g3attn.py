@@ -96,6 +96,7 @@ def lib():
     L.g3attn_last_error.restype = C.c_char_p
     L.g3attn_profile_enable.argtypes = [_vp, C.c_int]
     L.g3attn_profile_read.argtypes = [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int)]
+    L.g3attn_last_splits.argtypes = [_vp, C.c_int, C.POINTER(C.c_int)]
     L.g3attn_matvec_bf16.argtypes = [_f32p, _vp, _f32p, C.c_int, C.c_int, _vp]
     L.g3attn_matvec_bf16.restype = None
     L.g3attn_matvec_bf16_device.argtypes = [_vp, _vp, _vp, _vp, C.c_int, C.c_int]
@@ -120,7 +121,7 @@ def lib():
                  "g3attn_forward_device", "g3attn_upload_weights", "g3attn_forward_token",
                  "g3attn_prefill_tokens", "g3attn_matmul_bf16_device",
                  "g3attn_prefill_forward_device", "g3attn_forward_token_device",
-                 "g3attn_gqa_noalloc", "g3attn_upload_rope"):
+                 "g3attn_gqa_noalloc", "g3attn_upload_rope", "g3attn_last_splits"):
         getattr(L, name).restype = C.c_int
     _lib = L
     return L
@@ -317,6 +318,12 @@ class Context:
         ms, n = C.c_double(), C.c_int()
         _check(lib().g3attn_profile_read(self._h, kind, C.byref(ms), C.byref(n)))
         return ms.value, n.value
+
+    def last_splits(self, kind: int) -> int:
+        """Key splits the last call of kind 0 (decode) or 1 (prefill) chose."""
+        n = C.c_int()
+        _check(lib().g3attn_last_splits(self._h, kind, C.byref(n)))
+        return n.value
 
     def decode(self, layer, pos, q, k, v, q_norm=None, k_norm=None) -> np.ndarray:
         out = np.empty(self.qs, dtype=np.float32)

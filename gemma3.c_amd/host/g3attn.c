@@ -143,6 +143,7 @@ struct g3attn_ctx {
         double ms[2];
         int count[2];
     } prof;
+    int last_splits[2]; /* g3attn_last_splits: decode, prefill */
     int split_rows; /* 0 = heuristic */
     int min_rows;   /* smallest heuristic split */
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
@@ -457,6 +458,15 @@ int g3attn_profile_read(g3attn_ctx *c, int kind, double *total_ms, int *count) {
     return G3_OK;
 }
 
+int g3attn_last_splits(g3attn_ctx *c, int kind, int *splits) {
+    if (!c || kind < 0 || kind > 1 || !splits) {
+        set_err("g3attn_last_splits: bad arguments");
+        return G3_ERR_INVALID_ARG;
+    }
+    *splits = c->last_splits[kind];
+    return G3_OK;
+}
+
 /* ------------------------------------------------------------------ decode */
 
 /* Split-K shape: target_wgs workgroups (default two per compute unit,
@@ -576,6 +586,7 @@ static int decode_enqueue(g3attn_ctx *c, int layer, int pos, const float *q, con
     a.mask = NULL;
     a.qscale = (1.0f / sqrtf((float)D)) * LOG2E;
     choose_splits(a.n_stream, c->cfg.num_kv_heads, c->target_wgs, c->split_rows, c->min_rows, &a);
+    c->last_splits[0] = a.n_splits;
     a.n_kv_heads = c->cfg.num_kv_heads;
     a.group = c->group;
     a.out = attn_out;
@@ -959,6 +970,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.queries_per_wave = c->prefill_qpw;
     pa.schedule = c->prefill_sched;
     pa.ksplit = S;
+    c->last_splits[1] = S;
     pa.part_o = part_o;
     pa.part_ml = part_ml;
     pa.arrive = c->d_arrive;

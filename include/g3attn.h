@@ -172,7 +172,10 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
  * the process ends, so n_heads <= G3ATTN_NOALLOC_MAX_HEADS (larger calls
  * return -1 with a message).  Calls that overlap on one GPU (other streams,
  * other threads) race on that scratch; serialise them.  Same splits and
- * kernels as g3attn_gqa: the results agree bit for bit.  Returns 0 or -1. */
+ * kernels as g3attn_gqa: the results agree bit for bit.  The call enqueues
+ * kernel launches only (no allocation, no memset), so it can be recorded into
+ * a HIP graph once a first call on the device has run outside capture (that
+ * call looks the scratch address up).  Returns 0 or -1. */
 #define G3ATTN_NOALLOC_MAX_HEADS 16
 int g3attn_gqa_noalloc(float *output, const float *q, const float *k_cache, const float *v_cache,
                        int n_heads, int n_kv_heads, int seq_len, int head_dim, float scale,
@@ -329,6 +332,14 @@ int g3attn_synchronize(g3attn_ctx *ctx);
  * read and their summed duration in milliseconds, then resets that kind. */
 int g3attn_profile_enable(g3attn_ctx *ctx, int enable);
 int g3attn_profile_read(g3attn_ctx *ctx, int kind, double *total_ms, int *count);
+
+/* The work split the last call of one kind chose (no counterpart in the
+ * reference): kind 0, the decode's key splits per KV head (1 = no combine
+ * launch); kind 1, the prefill's key splits per query block (1, 2 or 4;
+ * above 1 the last split to arrive merges the parts inside the kernel).
+ * 0 before the first call of that kind.  For tests and benchmarks that must
+ * know which code path a call took. */
+int g3attn_last_splits(g3attn_ctx *ctx, int kind, int *splits);
 
 /* Thread-local message of the last failure on this thread ("" if none). */
 const char *g3attn_last_error(void);

@@ -18,7 +18,8 @@
 //   decode layer pos q k v q_norm k_norm out
 //   matmul N M K W X C                          (g3attn_matmul_bf16_device)
 //   gqa H Hkv seq q k v mask|- out              (g3attn_gqa, host pointers)
-//   gqa_noalloc H Hkv seq q k v mask|- out      (device copies, null stream)
+//   gqa_noalloc H Hkv seq q k v mask|- out      (device copies, null stream;
+//                                                fails if the call allocates)
 //   matvec M K A x y                            (g3attn_matvec_bf16, host)
 //   matvec_device M K A x y                     (g3attn_matvec_bf16_device)
 //   kv_append layer start n K V k_norm|-
@@ -31,6 +32,9 @@
 //   forward_token token pos logits              (the uploaded model)
 //   prefill_tokens n tokens start logits        (the uploaded model)
 //   destroy
+//   front_stage_only Hkv nk V vt_out            (g3k_rope_write_stage with an
+//                    empty batch, ra.n = 0, and no cache: the V^T staging of
+//                    nk keys alone; vt_out gets the bf16 hi plane [Hkv][256][ldk])
 //
 // At the end it prints "launch <kernel> <launches> <workgroups> <threads> <ms>" for every
 // kernel launched and "attn_emu: ok".
@@ -45,6 +49,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include "g3attn.h"
+#include "g3k.h"
 
 namespace {
 
@@ -272,7 +277,11 @@ int main(int argc, char **argv) {
             } else {
                 float *dq = to_device(q), *dk = to_device(k), *dv = to_device(v), *dout = to_device(out);
                 float *dm = mask.empty() ? nullptr : to_device(mask);
+                // the entry point allocates and frees nothing (its split
+                // partials live in the library's fixed device scratch)
+                const unsigned long long allocs = hostemu_alloc_calls();
                 check(g3attn_gqa_noalloc(dout, dq, dk, dv, h, hkv, seq, (int)D, scale, dm, nullptr), cmd);
+                if (hostemu_alloc_calls() != allocs) die("gqa_noalloc called an allocating entry point");
                 hipDeviceSynchronize();
                 hipMemcpy(out.data(), dout, out.size() * sizeof(float), hipMemcpyDeviceToHost);
                 for (void *p : {(void *)dq, (void *)dk, (void *)dv, (void *)dout, (void *)dm}) hipFree(p);
@@ -371,6 +380,46 @@ int main(int argc, char **argv) {
             std::vector<float> logits((size_t)vocab, -12345.0f);
             check(g3attn_prefill_tokens(ctx, tokens.data(), n, start, logits.data()), cmd);
             write_bin(lf, logits.data(), logits.size());
+        } else if (cmd == "front_stage_only") {
+            // The front launch with no batch tokens must stage V^T and touch
+            // nothing of the (absent) cache destination.
+            int hkv, nk;
+            std::string vf, of;
+            in >> hkv >> nk >> vf >> of;
+            if (!in || hkv < 1 || nk < 1) die("bad front_stage_only line");
+            const long long ldk = (nk + 63) / 64 * 64;
+            const auto V = read_bin<float>(vf, (size_t)nk * hkv * D);
+            float *dV = to_device(V);
+            std::vector<uint16_t> zero((size_t)hkv * D * ldk, 0), zk((size_t)hkv * ldk * 2 * D, 0);
+            uint16_t *dvt = to_device(zero), *dvl = to_device(zero), *dkq = to_device(zk);
+            std::vector<int> flag(1, 0);
+            int *dflag = to_device(flag);
+            g3k_rope_write_args ra;
+            std::memset(&ra, 0, sizeof ra);
+            ra.n = 0;
+            ra.n_kv_heads = hkv;
+            ra.V = dV;   // k_dst / v_dst stay NULL
+            g3k_stage_args sa;
+            std::memset(&sa, 0, sizeof sa);
+            sa.v_src = dV;
+            sa.head_stride = D;
+            sa.row_stride = (long long)hkv * D;
+            sa.kk0 = 0;
+            sa.cnt = (int)ldk;
+            sa.nk = nk;
+            sa.n_kv_heads = hkv;
+            sa.kq = dkq;
+            sa.vt = dvt;
+            sa.vt_lo = dvl;
+            sa.ldk = ldk;
+            sa.v_lo_flag = dflag;
+            sa.epoch = 1;
+            const int rc = g3k_rope_write_stage(&ra, &sa, nullptr);
+            if (rc) die("g3k_rope_write_stage returned " + std::to_string(rc));
+            std::vector<uint16_t> vt(zero.size());
+            hipMemcpy(vt.data(), dvt, vt.size() * sizeof(uint16_t), hipMemcpyDeviceToHost);
+            write_bin(of, vt.data(), vt.size());
+            for (void *p : {(void *)dV, (void *)dvt, (void *)dvl, (void *)dkq, (void *)dflag}) hipFree(p);
         } else if (cmd == "destroy") {
             g3attn_destroy(ctx);
             ctx = nullptr;

@@ -77,6 +77,9 @@ hipError_t hipGetSymbolAddress(void **p, const void *symbol);
  * hostemu_print_launches writes
  * "launch <name> <launches> <workgroups> <threads> <ms>" lines to stdout. */
 void hostemu_count_launch(const char *name, unsigned workgroups, unsigned threads, double ms);
+/* Calls of the allocating and freeing entry points above (hipMalloc,
+ * hipFree, hipHostMalloc, hipHostFree) since the process started. */
+unsigned long long hostemu_alloc_calls(void);
 double hostemu_now_ms(void);
 void hostemu_print_launches(void);
 

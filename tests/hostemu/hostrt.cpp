@@ -68,6 +68,8 @@ double now_ms() {
     return duration<double, std::milli>(steady_clock::now().time_since_epoch()).count();
 }
 
+unsigned long long g_alloc_calls = 0;   // hipMalloc / hipFree / hipHostMalloc / hipHostFree
+
 void *aligned(size_t bytes) {
     // 256-byte alignment, as hipMalloc gives, and exactly the requested size
     // (at least one byte), so AddressSanitizer flags any access past it even
@@ -113,21 +115,26 @@ hipError_t hipDeviceGetAttribute(int *v, hipDeviceAttribute_t attr, int device) 
 hipError_t hipDeviceSynchronize(void) { return hipSuccess; }
 
 hipError_t hipMalloc(void **p, size_t bytes) {
+    g_alloc_calls++;
     *p = aligned(bytes);
     return *p ? hipSuccess : hipErrorOutOfMemory;
 }
 hipError_t hipFree(void *p) {
+    g_alloc_calls++;
     std::free(p);
     return hipSuccess;
 }
 hipError_t hipHostMalloc(void **p, size_t bytes, unsigned) {
+    g_alloc_calls++;
     *p = aligned(bytes);
     return *p ? hipSuccess : hipErrorOutOfMemory;
 }
 hipError_t hipHostFree(void *p) {
+    g_alloc_calls++;
     std::free(p);
     return hipSuccess;
 }
+unsigned long long hostemu_alloc_calls(void) { return g_alloc_calls; }
 hipError_t hipMemcpy(void *dst, const void *src, size_t bytes, hipMemcpyKind) {
     if (bytes) std::memcpy(dst, src, bytes);
     return hipSuccess;

@@ -513,3 +513,22 @@ def test_upload_batched_prefill_then_decode(built, tmp_path):
     e.logits("forward_token", f"{int(tokens[n - 1])} {n - 1}", want[n - 1], f"forward_token {n - 1}")
     launches = e.run()
     assert launches["gemm_kernel"][0] > 0 and launches["rows_kernel"][0] > 0, launches
+
+
+def test_front_launch_with_an_empty_batch(built, tmp_path):
+    """The prefill front launch (g3k_rope_write_stage) called with an empty
+    batch (ra.n = 0) and no cache destination: its staging blocks still stage
+    V^T (bf16 hi plane, zero padding to the 64-key grain) and, under the
+    sanitizers, write nothing through the absent cache pointers."""
+    hkv, nk = 2, 70
+    e = Emu(tmp_path, H=4, Hkv=hkv)
+    V = _bf16_valued(e.rng.standard_normal((nk, hkv * D)))
+    e._save("Vs.bin", V)
+    e.lines.append(f"front_stage_only {hkv} {nk} Vs.bin vt.bin")
+    e.run()
+    ldk = (nk + 63) // 64 * 64
+    got = np.fromfile(os.path.join(e.dir, "vt.bin"), dtype=np.uint16).reshape(hkv, D, ldk)
+    bits = (V.view(np.uint32) >> 16).astype(np.uint16).reshape(nk, hkv, D)
+    want = np.zeros((hkv, D, ldk), np.uint16)
+    want[:, :, :nk] = bits.transpose(1, 2, 0)
+    assert np.array_equal(got, want)

@@ -119,10 +119,12 @@ def test_engine_falls_back_when_create_fails(monkeypatch):
 @needs_engine
 def test_engine_without_a_device_uses_the_cpu():
     """No GPU visible (this container): init fails on the device check and the
-    engine's CPU path runs every token."""
-    import torch
-    if torch.cuda.is_available():
-        pytest.skip("a GPU is visible")
+    engine's CPU path runs every token.  Whether a device is visible is
+    decided by the backend library itself (gemma3_metal_available: its own
+    hipGetDeviceCount through the HIP runtime libg3attn links), not by
+    another runtime's view of the machine."""
+    if C.CDLL(BACKEND_SO).gemma3_metal_available():
+        pytest.skip("the backend library sees a HIP device")
     rc, on_gpu, logits = run_engine(n_prefill=0)
     assert rc == 0 and on_gpu == 0
     assert "no HIP device" in g3attn().last_error()

@@ -53,8 +53,9 @@ def test_config1_local_decode(ctx8k):
 
 
 def test_cache_rewritten_by_copy(ctx8k):
-    """Cache rows that a decode has read, then rewritten by a host -> device
-    copy (g3attn_kv_write), are read back fresh by the next decode: two
+    """Cache rows that a decode has read, then rewritten through
+    g3attn_kv_write (a host -> device copy into staging, then the scatter
+    kernel into the cache), are read back fresh by the next decode: two
     different histories in the same slots, each against its own oracle."""
     for layer_seed in (0, 7, 0):
         _check(DecodeCase(1, layer=11, pos=700, max_context=8192, layer_seed=layer_seed), ctx8k,

@@ -327,12 +327,16 @@ def test_split_merge_repeats_in_one_context(ctx8k):
     call.  Alternating a 2-split local prefill (configs[2]'s shape) and a
     4-split 2048-token global prefill three times in one context reuses the
     counters with a changing split count; every repeat matches the first bit
-    for bit, and the first matches the oracle."""
+    for bit, and the first matches the oracle.  The split count each call
+    chose is read back from the library (g3attn_last_splits), so a change of
+    the split model cannot silently stop this test from merging in-kernel."""
     cases = [PrefillCase(70, layer=2, start_pos=0, n=2048), PrefillCase(71, layer=5, start_pos=0, n=2048)]
+    want_splits = (2, 4)
     first = []
     for rep in range(3):
         for i, case in enumerate(cases):
             got = case.gpu(ctx8k)
+            assert ctx8k.last_splits(1) == want_splits[i], (i, ctx8k.last_splits(1))
             if rep == 0:
                 want, _, _ = case.oracle()
                 err = rel_err(got, want)

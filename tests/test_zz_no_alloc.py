@@ -72,43 +72,59 @@ def test_noalloc_rejects_oversize():
             b.free()
 
 
+
 def test_noalloc_under_graph_capture():
-    """g3attn_gqa_noalloc recorded into a HIP graph (torch's CUDAGraph capture,
-    launched on torch's capture stream) and replayed three times.  Before each
+    """g3attn_gqa_noalloc recorded into a HIP graph (stream capture through the
+    HIP runtime the library links) and replayed three times.  Before each
     replay a new query is copied into the captured input buffer, and eager
     work (the copy, an allocating g3attn_gqa call) runs between replays; every
     replay matches the eager g3attn_gqa of its query bit for bit.  The call
     records kernel launches only: no allocation, no memset node."""
-    import torch
+    import ctypes as C
 
-    dev = torch.device("cuda:0")
+    hip = DeviceBuffer.hip()
+    vp = C.c_void_p
+    hip.hipStreamCreate.argtypes = [C.POINTER(vp)]
+    hip.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+    hip.hipStreamEndCapture.argtypes = [vp, C.POINTER(vp)]
+    hip.hipGraphInstantiate.argtypes = [C.POINTER(vp), vp, vp, vp, C.c_size_t]
+    hip.hipGraphLaunch.argtypes = [vp, vp]
+    hip.hipStreamSynchronize.argtypes = [vp]
+    for f in ("hipGraphExecDestroy", "hipGraphDestroy", "hipStreamDestroy"):
+        getattr(hip, f).argtypes = [vp]
+
     seq_len, n_heads, n_kv = 2048, 8, 4
     q, k, v = _inputs(seq_len, n_heads, n_kv, 0xC0DE)
-    tq, tk, tv = (torch.from_numpy(x).to(dev) for x in (q, k, v))
-    out = torch.zeros(n_heads * 256, device=dev, dtype=torch.float32)
+    bq, bk, bv = DeviceBuffer.of(q), DeviceBuffer.of(k), DeviceBuffer.of(v)
+    out = DeviceBuffer(n_heads * 256 * 4)
+    stream, graph, exe = vp(), vp(), vp()
+    assert hip.hipStreamCreate(C.byref(stream)) == 0
+    try:
+        def call():
+            G.gqa_noalloc(out.ptr, bq.ptr, bk.ptr, bv.ptr, n_heads, n_kv, seq_len, stream=stream.value)
 
-    def call(stream):
-        G.gqa_noalloc(out.data_ptr(), tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), n_heads, n_kv, seq_len,
-                      stream=stream)
-
-    # the first call on a device looks its scratch address up: do it eagerly
-    side = torch.cuda.Stream()
-    with torch.cuda.stream(side):
-        call(side.cuda_stream)
-    side.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        call(torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
-    for rep in range(3):
-        qr = O.gen_normal_bf16(n_heads * 256, 0xC0DE + 97 * (rep + 1))
-        tq.copy_(torch.from_numpy(qr).to(dev))
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        got = out.cpu().numpy()
-        ref = G.gqa(qr, k, v, n_heads, n_kv, seq_len)
-        print(f"[noalloc graph] replay {rep}: max |diff| vs eager = "
-              f"{float(np.max(np.abs(got - ref))):.3e}", flush=True)
-        assert np.array_equal(got, ref), rep
-    del graph
+        # the first call on a device looks its scratch address up: run it eagerly
+        call()
+        assert hip.hipStreamSynchronize(stream) == 0
+        assert hip.hipStreamBeginCapture(stream, 2) == 0     # hipStreamCaptureModeRelaxed
+        call()
+        assert hip.hipStreamEndCapture(stream, C.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        for rep in range(3):
+            qr = O.gen_normal_bf16(n_heads * 256, 0xC0DE + 97 * (rep + 1))
+            bq.upload(qr)
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            got = out.download(np.float32, n_heads * 256)
+            ref = G.gqa(qr, k, v, n_heads, n_kv, seq_len)
+            print(f"[noalloc graph] replay {rep}: max |diff| vs eager = "
+                  f"{float(np.max(np.abs(got - ref))):.3e}", flush=True)
+            assert np.array_equal(got, ref), rep
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        hip.hipStreamDestroy(stream)
+        for b in (bq, bk, bv, out):
+            b.free()

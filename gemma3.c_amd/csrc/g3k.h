@@ -86,12 +86,25 @@ typedef struct {
     int ring;              /* >0: slot = pos % ring; 0: slot = pos - dst_pos0 */
     int dst_pos0;
     int kv_skip;           /* tokens i < kv_skip are not written to k_dst / v_dst */
-    /* optional prefill staging of the rotated keys, fp16 hi | lo rows
-     * (bit patterns), kq [n_kv_heads][ldk][2][D], token i at row row0 + i */
+    /* optional prefill staging of the rotated keys (bit patterns),
+     * kq [n_kv_heads][ldk][2][D], token i at row row0 + i: fp16 hi | lo rows,
+     * or, with kscale != NULL, fp16 hi | fp8 cross rows and the row's scale
+     * byte in kscale [n_kv_heads][ldk] (see G3K_KROW_X8) */
     uint16_t *kq;
+    uint8_t *kscale;
     long long ldk;
     int row0;
 } g3k_rope_write_args;
+
+/* Key row formats of the prefill staging (1 KiB per key and KV head).
+ * Exact policy: fp16 hi (dim d at bytes 2d) | fp16 lo = fp16(k - hi) (512 +
+ * 2d).  Fp8 cross policy (G3K_KROW_X8): fp16 hi as above | 512 bytes of OCP
+ * e4m3 in the lane order of the 16x16x128 fp8 MFMA: part p (0: hi / 2^E,
+ * 1: lo * 2^11 / 2^E, lo = k - hi in fp32) of dim d = 32 t + 8 g + u at byte
+ * 512 + 256 p + 64 (t >> 1) + 16 g + 8 (t & 1) + u, where E = floor(log2
+ * max |k|) - 7 over the row (0 for a zero row) keeps every value within
+ * +-256; the row's scale byte is the E8M0 code 127 + E. */
+#define G3K_KROW_X8 1
 
 int g3k_rope_write(const g3k_rope_write_args *a, void *stream);
 
@@ -103,8 +116,10 @@ int g3k_kv_scatter(float *dst_k, float *dst_v, float *rows_k, float *rows_v, int
                    long long head_stride, int slot, int to_rows, void *stream);
 
 /* Prefill staging of key rows kk0..kk0+cnt-1 (key index kk = position -
- * kstart): K (already normed + rotated, fp32) -> fp16 hi | lo rows of
- * kq [H_kv][ldk][2][D]; V (fp32) -> bf16 hi and lo columns of vt / vt_lo
+ * kstart): K (already normed + rotated, fp32) -> key rows of
+ * kq [H_kv][ldk][2][D] in the format kscale selects (exact fp16 hi | lo, or
+ * fp16 hi | fp8 cross with a scale byte per row, G3K_KROW_X8); V (fp32) ->
+ * bf16 hi and lo columns of vt / vt_lo
  * [H_kv][D][ldk] (v = hi + lo to 16 bits).  If any staged V has a nonzero lo
  * part, *v_lo_flag is set to epoch.
  * Source row of key kk (position pos = kstart + kk) for head h:
@@ -117,6 +132,7 @@ typedef struct {
     int ring, row_pos0, kstart;
     int kk0, cnt, nk, n_kv_heads;
     uint16_t *kq, *vt, *vt_lo;
+    uint8_t *kscale;       /* NULL: exact key rows; else fp8 cross rows + scale bytes */
     long long ldk;
     int *v_lo_flag;
     int epoch;
@@ -134,7 +150,8 @@ int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_stage_args *sa
  *   q:  raw (pre-norm) queries [n][n_heads][D] fp32, the reference's Q_all
  *       layout; the kernel applies QK-norm (q_norm, NULL = none) and RoPE
  *       (table row start_pos + i) to token i, whose key index is hist + i.
- *   kq: fp16 split keys [H_kv][ldk][2][D] (hi | lo rows); vt / vt_lo: bf16
+ *   kq: staged keys [H_kv][ldk][2][D] in the row format kscale selects
+ *       (exact or fp8 cross, G3K_KROW_X8); vt / vt_lo: bf16
  *       hi / lo values [H_kv][D][ldk], nk valid key indices, zero padded to
  *       ldk (a multiple of 64).  vt_lo is read only when *v_lo_flag == epoch
  *       (some staged V is not exactly bf16).
@@ -147,6 +164,7 @@ typedef struct {
     float eps;
     int start_pos;
     const uint16_t *kq, *vt, *vt_lo;
+    const uint8_t *kscale;    /* NULL: exact key rows; else fp8 cross rows + scale bytes */
     const int *v_lo_flag;
     int epoch;
     float *out;

@@ -57,6 +57,32 @@ __device__ __forceinline__ float col4_max(float v) { return pair16_max(pair32_ma
 // Sum over all 64 lanes; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) { return col4_sum(row16_sum(v)); }
 
+// Max over the 16 lanes of a DPP row, then over all 64 lanes.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) { return col4_max(row16_max(v)); }
+
+// Power-of-two scale of a block of values whose largest magnitude is m: the
+// exponent E = floor(log2 m) - 7, so every value / 2^E lies within +-256
+// (OCP e4m3 holds +-448), clamped to [-126, 127]; E = 0 for m = 0.
+__device__ __forceinline__ int x8_exponent(float m) {
+    if (!(m > 0.f)) return 0;
+    const int e = __builtin_amdgcn_frexp_expf(m) - 8;   // m = f 2^k, f in [0.5, 1): floor(log2 m) = k - 1
+    return e < -126 ? -126 : (e > 127 ? 127 : e);
+}
+
+// Two floats -> two OCP e4m3 codes (round to nearest even) in the low 16
+// bits, or, with hi, in the high 16 bits of `old` (v_cvt_pk_fp8_f32).
+__device__ __forceinline__ uint32_t e4m3_pair(float a, float b, uint32_t old = 0, bool hi = false) {
+    return hi ? (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, true)
+              : (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, false);
+}
+
 // v_exp_f32: 2^x, flushes to 0 for very negative x.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -66,6 +66,9 @@ constexpr int KTILEB = BK * KROWB;           // bytes of a K tile (32768)
 constexpr int VTILEB = D * BK * 2;           // bytes of a V^T tile, one part (16 KiB)
 constexpr int LDS_V0 = 2 * KTILEB;           // V ring after the K ring
 constexpr int LDS_BYTES = LDS_V0 + 2 * 2 * VTILEB;   // 131072
+constexpr int LDS_KS0 = LDS_BYTES;           // fp8 cross policy: key-scale ring after the V ring
+constexpr int KS_SLOT = 256;                 // one tile's 32 scale bytes (a 256-byte fetch)
+constexpr int LDS_BYTES_X8 = LDS_KS0 + 2 * KS_SLOT;
 constexpr float NEG_BIG = -1.0e30f;
 constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 #ifndef G3K_KPF
@@ -76,18 +79,25 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+// 32 fp8 bytes of an MFMA operand from two 16-byte pieces (bytes 0-15, 16-31)
+__device__ __forceinline__ i32x8 cat8(u32x4 a, u32x4 b) {
+    return __builtin_bit_cast(i32x8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 // Cache-policy bits of a buffer access: sc1, agent-coherent (written through
 // to / read from the point of coherence shared by every XCD).
 constexpr int CP_SC1 = 16;
 
-__device__ __forceinline__ uint16_t f16_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ uint16_t bf16_bits(__bf16 h) { return __builtin_bit_cast(uint16_t, h); }
 
 // ---------------------------------------------------------------------------
-// Staging: fp32 K rows -> fp16 hi | lo rows, fp32 V rows -> bf16 hi and lo
-// V^T columns.  Workgroup = 64 keys x 64 dims of one head (grid: key blocks,
-// D/64, H_kv).
+// Staging: fp32 V rows -> bf16 hi and lo V^T columns (workgroups of 64 keys
+// x 64 dims of one head); fp32 K rows -> key rows in the policy's format
+// (write_krow: one wave per key row, which holds the whole row for the fp8
+// format's per-row scale).
 // ---------------------------------------------------------------------------
 // vc != nullptr (the prefill front launch, staging the batch's own V): the
 // staged V values are also written to the cache rows vc describes
@@ -106,33 +116,17 @@ __device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int
         const int r = c >> 4, col = (c & 15) * 4;
         const int kk = kkbase + r;
         if (kk >= kend) continue;
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+        float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (kk < a.nk) {
             const int pos = a.kstart + kk;
             const long long row = a.ring > 0 ? pos % a.ring : pos - a.row_pos0;
             const size_t off = (size_t)h * a.head_stride + (size_t)row * a.row_stride + dx * 64 + col;
             vv = *reinterpret_cast<const float4 *>(a.v_src + off);
-            if (a.k_src) kv = *reinterpret_cast<const float4 *>(a.k_src + off);
             if (vc && pos - vc->start_pos >= vc->kv_skip && pos - vc->start_pos < vc->n) {
                 const int slot = vc->ring > 0 ? pos % vc->ring : pos - vc->dst_pos0;
                 *reinterpret_cast<float4 *>(vc->v_dst + (size_t)h * vc->dst_head_stride + (size_t)slot * D + dx * 64 +
                                             col) = vv;
             }
-        }
-        if (a.k_src || kk >= a.nk) {
-            const float x[4] = {kv.x, kv.y, kv.z, kv.w};
-            uint16_t hi[4], lo[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const _Float16 xh = (_Float16)x[e];
-                hi[e] = f16_bits(xh);
-                lo[e] = f16_bits((_Float16)(x[e] - (float)xh));
-            }
-            uint16_t *row = a.kq + ((size_t)h * a.ldk + kk) * (2 * D) + dx * 64 + col;
-            *reinterpret_cast<uint2 *>(row) =
-                make_uint2(hi[0] | (uint32_t)hi[1] << 16, hi[2] | (uint32_t)hi[3] << 16);
-            *reinterpret_cast<uint2 *>(row + D) =
-                make_uint2(lo[0] | (uint32_t)lo[1] << 16, lo[2] | (uint32_t)lo[3] << 16);
         }
         const float y[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
@@ -169,21 +163,65 @@ __device__ __forceinline__ void stage_block(const g3k_stage_args &a, int kb, int
     }
 }
 
-__global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a) { stage_block(a, blockIdx.x, blockIdx.y, blockIdx.z); }
+// Key rows of the staging (one wave each): the first key index whose row
+// this launch writes, and how many (times the KV heads).  With k_src every
+// row of [kk0, kk0 + cnt) (from the cache below nk, zeros above); without it
+// (the batch's own keys come from rope_write_vec) only the zero padding rows
+// from nk on.
+__device__ __host__ __forceinline__ int krow_first(const g3k_stage_args &a) {
+    return a.k_src ? a.kk0 : (a.nk > a.kk0 ? a.nk : a.kk0);
+}
+__device__ __host__ __forceinline__ long long krow_count(const g3k_stage_args &a) {
+    const int n = a.kk0 + a.cnt - krow_first(a);
+    return n > 0 ? (long long)n * a.n_kv_heads : 0;
+}
+
+// Key row w (of krow_count) of the staging: key index kk = krow_first + w /
+// H_kv, head w % H_kv.
+__device__ __forceinline__ void stage_krow(const g3k_stage_args &a, long long w, int lane) {
+    if (w >= krow_count(a)) return;
+    const int kk = krow_first(a) + (int)(w / a.n_kv_heads), h = (int)(w % a.n_kv_heads);
+    float2 lo = make_float2(0.f, 0.f), hi = lo;
+    if (a.k_src && kk < a.nk) {
+        const int pos = a.kstart + kk;
+        const long long row = a.ring > 0 ? pos % a.ring : pos - a.row_pos0;
+        const float *src = a.k_src + (size_t)h * a.head_stride + (size_t)row * a.row_stride;
+        lo = *reinterpret_cast<const float2 *>(src + 2 * lane);
+        hi = *reinterpret_cast<const float2 *>(src + 128 + 2 * lane);
+    }
+    const size_t r = (size_t)h * a.ldk + kk;
+    write_krow(a.kq + r * (2 * D), a.kscale ? a.kscale + r : nullptr, lo.x, lo.y, hi.x, hi.y, lane);
+}
+
+// History staging in one launch: the V^T blocks (key blocks x D / 64 x H_kv,
+// first) and the key-row waves (four per workgroup).
+__global__ __launch_bounds__(NT) void stage_kernel(g3k_stage_args a, unsigned vblocks, unsigned kblocks) {
+    const unsigned b = blockIdx.x;
+    if (b < vblocks) {
+        const unsigned per_head = kblocks * (D / 64);
+        stage_block(a, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head));
+        return;
+    }
+    stage_krow(a, ((long long)(b - vblocks) * NT + threadIdx.x) >> 6, threadIdx.x & 63);
+}
 
 // The batch's front end in one launch: the V^T staging blocks of `sa` (first:
-// fewer and heavier), which also write the batch's V rows to the cache, and
-// the K waves of rope_write_vec over `ra` (K-norm, RoPE, cache write, fp16
-// hi | lo key rows).  The two read disjoint inputs (V / K) and write
-// disjoint buffers, so their order does not matter.
+// fewer and heavier), which also write the batch's V rows to the cache, the
+// K waves of rope_write_vec over `ra` (K-norm, RoPE, cache write, staged key
+// rows), then the zero key rows of the padding.  The parts read disjoint
+// inputs (V / K) and write disjoint buffers, so their order does not matter.
 __global__ __launch_bounds__(NT) void front_kernel(g3k_rope_write_args ra, g3k_stage_args sa, unsigned stage_blocks,
-                                                   unsigned kblocks) {
+                                                   unsigned kblocks, unsigned rw_blocks) {
     const unsigned b = blockIdx.x;
     if (b < stage_blocks) {
         const unsigned per_head = kblocks * (D / 64);
         // the cache rows are written only for a batch that has tokens
         stage_block(sa, (int)(b % kblocks), (int)((b % per_head) / kblocks), (int)(b / per_head),
                     ra.n > 0 ? &ra : nullptr);
+        return;
+    }
+    if (b >= stage_blocks + rw_blocks) {
+        stage_krow(sa, ((long long)(b - stage_blocks - rw_blocks) * NT + threadIdx.x) >> 6, threadIdx.x & 63);
         return;
     }
     // K wave kw = token i x H_kv + head h is rope_write_vec's vector i x
@@ -256,23 +294,49 @@ __device__ __forceinline__ void wait_fetch_all() { G3K_WAIT_VMEM(); }
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // S^T of one key tile for this wave's NQB blocks of 16 queries: keys 0-15
-// (s[b][0]) and 16-31 (s[b][1]) of the tile, three fp16 passes (k_hi q_hi,
-// k_hi q_lo, k_lo q_hi).  Every K fragment read from LDS feeds all NQB query
-// blocks; the fragments of d-step t + 1 are read while step t's MFMAs run.
-template <int NQB>
+// (s[b][0]) and 16-31 (s[b][1]) of the tile.  Every K fragment read from LDS
+// feeds all NQB query blocks; the fragments of step t + 1 are read while
+// step t's MFMAs run.
+//   Exact policy (X8 = false): three fp16 passes per 32-dim step (k_hi q_hi,
+//     k_hi q_lo, k_lo q_hi); qlo holds fp16 q_lo.
+//   Fp8 cross policy (X8): one fp16 pass k_hi q_hi over the 8 dim steps, and
+//     the cross terms k_hi q_lo + k_lo q_hi as four scaled fp8 MFMAs
+//     (v_mfma_scale_f32_16x16x128_f8f6f4, OCP e4m3) over the rows' fp8 half:
+//     MFMA j (part p = j / 2: k_hi with q_lo, then k_lo with q_hi) takes the
+//     row's 16-byte chunks 8 + 2 j and 9 + 2 j and the query's fp8 bytes
+//     qlo[b][2 j], qlo[b][2 j + 1].  The E8M0 scales (key row: sa, query:
+//     sb[b]) undo the per-row and per-query exponents and the 2^11 of the
+//     low parts, so the cross terms land in the same fp32 accumulator as
+//     the fp16 pass.  Eight steps of four fragment reads each: the fp16
+//     passes two dim steps at a time, alternating with the fp8 MFMAs.
+template <int NQB, bool X8>
 __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned char *st, const int (&ka)[4],
                                             const int (&kb)[4], const half8 (&qh)[NQB][8],
-                                            const half8 (&ql)[NQB][8]) {
-    constexpr int PF = G3K_KPF;       // d-steps of K fragments in flight
+                                            const u32x4 (&qlo)[NQB][8], const unsigned char *ks, int krow,
+                                            const int (&sb)[NQB]) {
+    constexpr int PF = G3K_KPF;       // steps of K fragments in flight
 #pragma unroll
     for (int b = 0; b < NQB; b++) s[b][0] = s[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    half8 f[PF + 1][4];
-    auto load = [&](half8 (&r)[4], int t) {
-        r[0] = *reinterpret_cast<const half8 *>(st + ka[t & 3] + 256 * (t >> 2));
-        r[1] = *reinterpret_cast<const half8 *>(st + ka[t & 3] + 512 + 256 * (t >> 2));
-        r[2] = *reinterpret_cast<const half8 *>(st + kb[t & 3] + 256 * (t >> 2));
-        r[3] = *reinterpret_cast<const half8 *>(st + kb[t & 3] + 512 + 256 * (t >> 2));
+    u32x4 f[PF + 1][4];
+    // chunk t (16 bytes of lane group g) of the sub-tile 0 / 1 rows
+    auto c0 = [&](int t) { return *reinterpret_cast<const u32x4 *>(st + ka[t & 3] + 256 * (t >> 2)); };
+    auto c1 = [&](int t) { return *reinterpret_cast<const u32x4 *>(st + kb[t & 3] + 256 * (t >> 2)); };
+    auto load = [&](u32x4 (&r)[4], int t) {
+        if (!X8) {   // d-step t: hi and lo chunks of both sub-tiles
+            r[0] = c0(t); r[1] = c0(t + 8); r[2] = c1(t); r[3] = c1(t + 8);
+        } else if ((t & 1) == 0) {   // d-steps t, t + 1 of the fp16 hi pass
+            r[0] = c0(t); r[1] = c1(t); r[2] = c0(t + 1); r[3] = c1(t + 1);
+        } else {     // fp8 MFMA j = t / 2: chunks 8 + 2 j, 9 + 2 j
+            const int j = t >> 1;
+            r[0] = c0(8 + 2 * j); r[1] = c0(9 + 2 * j); r[2] = c1(8 + 2 * j); r[3] = c1(9 + 2 * j);
+        }
     };
+    // this lane's key rows' scale bytes (sub-tile 0: krow, 1: krow + 4)
+    int sa0 = 0, sa1 = 0;
+    if (X8) {
+        sa0 = ks[krow];
+        sa1 = ks[krow + 4];
+    }
 #pragma unroll
     for (int t = 0; t < PF; t++) load(f[t], t);
     // issue priority for the score MFMAs over the other wave of the SIMD
@@ -286,12 +350,29 @@ __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned c
         sched_fence();
 #pragma unroll
         for (int b = 0; b < NQB; b++) {
-            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], qh[b][t], s[b][0], 0, 0, 0);
-            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], qh[b][t], s[b][1], 0, 0, 0);
-            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][0], ql[b][t], s[b][0], 0, 0, 0);
-            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][2], ql[b][t], s[b][1], 0, 0, 0);
-            s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][1], qh[b][t], s[b][0], 0, 0, 0);
-            s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[c][3], qh[b][t], s[b][1], 0, 0, 0);
+            if (!X8) {
+                const half8 kh0 = as_half8(f[c][0]), kl0 = as_half8(f[c][1]);
+                const half8 kh1 = as_half8(f[c][2]), kl1 = as_half8(f[c][3]);
+                const half8 ql = as_half8(qlo[b][t]);
+                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, qh[b][t], s[b][0], 0, 0, 0);
+                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, qh[b][t], s[b][1], 0, 0, 0);
+                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh0, ql, s[b][0], 0, 0, 0);
+                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh1, ql, s[b][1], 0, 0, 0);
+                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl0, qh[b][t], s[b][0], 0, 0, 0);
+                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl1, qh[b][t], s[b][1], 0, 0, 0);
+            } else if ((t & 1) == 0) {
+                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(f[c][0]), qh[b][t], s[b][0], 0, 0, 0);
+                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(f[c][1]), qh[b][t], s[b][1], 0, 0, 0);
+                s[b][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(f[c][2]), qh[b][t + 1], s[b][0], 0, 0, 0);
+                s[b][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(f[c][3]), qh[b][t + 1], s[b][1], 0, 0, 0);
+            } else {
+                const int j = t >> 1;
+                const i32x8 qx = cat8(qlo[b][2 * j], qlo[b][2 * j + 1]);
+                s[b][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cat8(f[c][0], f[c][1]), qx, s[b][0], 0, 0,
+                                                                           0, sa0, 0, sb[b]);
+                s[b][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cat8(f[c][2], f[c][3]), qx, s[b][1], 0, 0,
+                                                                           0, sa1, 0, sb[b]);
+            }
         }
         sched_fence();
     }
@@ -299,10 +380,18 @@ __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned c
 }
 
 // Loads, QK-norms and rotates (gemma3_kernels.c:289-304, 470-484) one block of
-// 16 queries into the B-operand layout and splits it into fp16 hi / lo.
+// 16 queries into the B-operand layout and splits it: qh = fp16(v), and in
+// qlo either fp16(v - qh) (exact policy) or, for the fp8 cross policy, the
+// query's fp8 operand bytes of the four cross MFMAs: MFMA j = 2 p + jj takes
+// part p (0: (v - qh) 2^11 / 2^E, 1: qh / 2^E) of dims 32 t + 8 g + u,
+// t = 4 jj .. 4 jj + 3, at byte 8 (t - 4 jj) + u of qlo[2 j] | qlo[2 j + 1]
+// (the key rows' fp8 bytes are in the same order), with E the query's
+// exponent (x8_exponent of its largest |v|) and sb the E8M0 code 127 + E -
+// 11 of the product scale.
 // Lane (ln, g) holds dims 32 t + 8 g + u; dim d < 128 and its RoPE partner
 // d + 128 are t and t + 4 of the same lane.
-__device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], const g3k_prefill_args &p,
+template <bool X8>
+__device__ __forceinline__ void load_queries(half8 (&qh)[8], u32x4 (&qlo)[8], int &sb, const g3k_prefill_args &p,
                                              int tok, int qhead, int n_heads, int g) {
     const bool qv = tok < p.n;
     const float *qrow = p.q + ((size_t)(qv ? tok : 0) * n_heads + qhead) * D + 8 * g;
@@ -361,6 +450,7 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
             }
         }
     }
+    float mloc = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++)
 #pragma unroll
@@ -368,13 +458,52 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], half8 (&ql)[8], con
             const float v = qv ? x[t][u] * p.qscale : 0.f;
             const _Float16 hi = (_Float16)v;
             qh[t][u] = hi;
-            ql[t][u] = (_Float16)(v - (float)hi);
+            x[t][u] = v - (float)hi;      // the low part, exact in fp32
+            mloc = fmaxf(mloc, fabsf(v));
         }
+    if (!X8) {
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            half8 l;
+#pragma unroll
+            for (int u = 0; u < 8; u++) l[u] = (_Float16)x[t][u];
+            qlo[t] = __builtin_bit_cast(u32x4, l);
+        }
+        sb = 0;
+        return;
+    }
+    // the query's exponent: its 256 dims are in the four lanes ln + 16 g;
+    // at least -115 so that the product scale's code 127 + E - 11 stays >= 1
+    int E = x8_exponent(col4_max(mloc));
+    E = E < -115 ? -115 : E;
+    sb = 127 + E - 11;
+    const float inv = __builtin_amdgcn_ldexpf(1.0f, -E), inv_lo = __builtin_amdgcn_ldexpf(1.0f, 11 - E);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int part = j >> 1, jj = j & 1;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            u32x4 w;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                // bytes 16 h + 4 k .. + 3: t = 4 jj + 2 h + k / 2, u = 4 (k % 2) .. + 3
+                const int t = 4 * jj + 2 * h + (k >> 1), u0 = 4 * (k & 1);
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    y[e] = part == 0 ? x[t][u0 + e] * inv_lo : (float)qh[t][u0 + e] * inv;
+                w[k] = e4m3_pair(y[2], y[3], e4m3_pair(y[0], y[1]), true);
+            }
+            qlo[2 * j + h] = w;
+        }
+    }
 }
 
 // One workgroup's attention: 8 / NQB waves, each owning NQB blocks of 16
-// queries of one head over the full head dim.  VLO adds the P_hi.V_lo pass.
-template <int G, int NQB, bool VLO>
+// queries of one head over the full head dim.  VLO adds the P_hi.V_lo pass;
+// X8 selects the fp8 cross policy of the scores (staged key rows in that
+// format, with a ring of the tiles' key-scale bytes after the V ring).
+template <int G, int NQB, bool VLO, bool X8>
 __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char *smem) {
     constexpr int NW = 8 / NQB;       // waves per workgroup
     constexpr int WPH = NW / G;       // waves per query head
@@ -429,17 +558,29 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         fetch_v<NW>(vbuf(kt), vr, kt, fwave, voff_v, ldk);
         if (VLO) fetch_v<NW>(vbuf(kt) + VTILEB, vlr, kt, fwave, voff_v, ldk);
     };
+    // fp8 cross policy: tile kt's 32 key-scale bytes -> its scale slot, one
+    // 4-byte buffer -> LDS fetch per lane of wave 0 (the 256 bytes past the
+    // tile's 32 are unused; past the head's ldk bytes they read as zero)
+    const __amdgpu_buffer_rsrc_t ksr = make_rsrc(X8 ? (const void *)(p.kscale + (size_t)kvh * ldk) : (const void *)p.kq, (unsigned)ldk);
+    auto ksbuf = [&](int kt) { return smem + LDS_KS0 + (kt & 1) * KS_SLOT; };
+    auto fetch_kt = [&](int kt) {
+        fetch_k<NW>(kbuf(kt), kr, kt, fwave, lane);
+        if (X8 && fwave == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ksr, (lds_ptr)ksbuf(kt), 4, lane * 4, kt * BK, 0, 0);
+    };
 
     // ---- K of the first two tiles and V of the first in flight, then this
     // wave's queries ----
-    fetch_k<NW>(kbuf(kt0), kr, kt0, fwave, lane);
-    if (kt0 + 1 <= kt1) fetch_k<NW>(kbuf(kt0 + 1), kr, kt0 + 1, fwave, lane);
+    fetch_kt(kt0);
+    if (kt0 + 1 <= kt1) fetch_kt(kt0 + 1);
     fetch_vt(kt0);
 
-    half8 qh[NQB][8], ql[NQB][8];
+    half8 qh[NQB][8];
+    u32x4 qlo[NQB][8];
+    int sb[NQB];
 #pragma unroll
     for (int b = 0; b < NQB; b++)
-        load_queries(qh[b], ql[b], p, tok0 + 16 * b + ln, qhead, p.n_kv_heads * G, g);
+        load_queries<X8>(qh[b], qlo[b], sb[b], p, tok0 + 16 * b + ln, qhead, p.n_kv_heads * G, g);
 
     f32x4 o[NQB][16];
     float m_ref[NQB], l_sum[NQB];
@@ -474,7 +615,8 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // Software pipeline: iteration kt issues tile kt+1's S^T MFMAs and tile
     // kt's softmax + P.V (in either order, see `late`).
     f32x4 s[NQB][2];
-    if (wave_live && kt0 >= wkt0 && kt0 <= wkt1) tile_scores<NQB>(s, kbuf(kt0), koff0, koff1, qh, ql);
+    if (wave_live && kt0 >= wkt0 && kt0 <= wkt1)
+        tile_scores<NQB, X8>(s, kbuf(kt0), koff0, koff1, qh, qlo, ksbuf(kt0), krow, sb);
     // the first iteration refills K tile kt0's slot: every wave must be done
     // reading it
     __syncthreads();
@@ -482,7 +624,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     for (int kt = kt0; kt <= kt1; kt++) {
         // K of tile kt + 2 replaces K of tile kt (scored last iteration), V
         // of tile kt + 1 replaces V of tile kt - 1
-        if (kt + 2 <= kt1) fetch_k<NW>(kbuf(kt + 2), kr, kt + 2, fwave, lane);
+        if (kt + 2 <= kt1) fetch_kt(kt + 2);
         if (kt + 1 <= kt1) fetch_vt(kt + 1);
         const unsigned char *vs = vbuf(kt);
 
@@ -491,7 +633,7 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         for (int b = 0; b < NQB; b++) sn[b][0] = s[b][0], sn[b][1] = s[b][1];
         auto scores_next = [&]() {
             if (wave_live && kt + 1 >= wkt0 && kt + 1 <= wkt1)
-                tile_scores<NQB>(sn, kbuf(kt + 1), koff0, koff1, qh, ql);
+                tile_scores<NQB, X8>(sn, kbuf(kt + 1), koff0, koff1, qh, qlo, ksbuf(kt + 1), krow, sb);
         };
         auto softmax_pv = [&]() {
           if (wave_live && kt >= wkt0 && kt <= wkt1) {
@@ -695,22 +837,27 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
 
 // The V_lo pass is taken when this call's staging found a V that is not
 // exactly bf16 (flag == epoch); the branch is uniform over the grid.
-template <int G, int NQB>
+template <int G, int NQB, bool X8>
 __global__ __launch_bounds__(512 / NQB, 1) void prefill_kernel(g3k_prefill_args p) {
-    __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char smem[X8 ? LDS_BYTES_X8 : LDS_BYTES];
     if (*p.v_lo_flag == p.epoch)
-        attend<G, NQB, true>(p, smem);
+        attend<G, NQB, true, X8>(p, smem);
     else
-        attend<G, NQB, false>(p, smem);
+        attend<G, NQB, false, X8>(p, smem);
 }
 
 template <int G, int NQB>
 hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
     constexpr int PB = 16 * NQB * ((8 / NQB) / G);
     const int nqb = (a->n + PB - 1) / PB;
+    const dim3 grid(nqb * a->n_kv_heads * a->ksplit);
     // With timing events the dispatch itself records them (kernel begin / end).
-    hipExtLaunchKernelGGL((prefill_kernel<G, NQB>), dim3(nqb * a->n_kv_heads * a->ksplit), dim3(512 / NQB), 0,
-                          st, (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
+    if (a->kscale)
+        hipExtLaunchKernelGGL((prefill_kernel<G, NQB, true>), grid, dim3(512 / NQB), 0, st, (hipEvent_t)a->ev0,
+                              (hipEvent_t)a->ev1, 0, *a);
+    else
+        hipExtLaunchKernelGGL((prefill_kernel<G, NQB, false>), grid, dim3(512 / NQB), 0, st, (hipEvent_t)a->ev0,
+                              (hipEvent_t)a->ev1, 0, *a);
     return hipGetLastError();
 }
 
@@ -719,8 +866,12 @@ hipError_t launch_prefill(const g3k_prefill_args *a, hipStream_t st) {
 extern "C" int g3k_stage(const g3k_stage_args *a, void *stream) {
     if (a->cnt <= 0) return 0;
     if (a->ldk % 64 || a->kk0 + a->cnt > a->ldk || !a->v_lo_flag) return (int)hipErrorInvalidValue;
-    dim3 grid((a->cnt + 63) / 64, D / 64, a->n_kv_heads);
-    hipLaunchKernelGGL(stage_kernel, grid, dim3(NT), 0, (hipStream_t)stream, *a);
+    const long long kblocks = (a->cnt + 63) / 64;
+    const long long vblocks = kblocks * (D / 64) * a->n_kv_heads;
+    const long long kr_blocks = (krow_count(*a) + 3) / 4;
+    if (vblocks + kr_blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(stage_kernel, dim3((unsigned)(vblocks + kr_blocks)), dim3(NT), 0, (hipStream_t)stream, *a,
+                       (unsigned)vblocks, (unsigned)kblocks);
     return (int)hipGetLastError();
 }
 
@@ -735,12 +886,14 @@ extern "C" int g3k_rope_write_stage(const g3k_rope_write_args *ra, const g3k_sta
     // start_pos ..) and read V from the batch's own rows
     if (ra->n > 0 && (sa->cnt < ra->n || sa->nk != sa->kk0 + ra->n || sa->k_src || sa->ring ||
                       sa->row_pos0 != ra->start_pos ||
-                      sa->kstart + sa->kk0 != ra->start_pos || sa->v_src != ra->V || sa->n_kv_heads != ra->n_kv_heads))
+                      sa->kstart + sa->kk0 != ra->start_pos || sa->v_src != ra->V || sa->n_kv_heads != ra->n_kv_heads ||
+                      ra->kq != sa->kq || ra->kscale != sa->kscale || ra->row0 != sa->kk0 || ra->ldk != sa->ldk))
         return (int)hipErrorInvalidValue;
     const long long rw_blocks = ra->n > 0 ? ((long long)ra->n * ra->n_kv_heads + 3) / 4 : 0;
-    if (stage_blocks + rw_blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(front_kernel, dim3((unsigned)(stage_blocks + rw_blocks)), dim3(NT), 0, (hipStream_t)stream, *ra,
-                       *sa, (unsigned)stage_blocks, (unsigned)kblocks);
+    const long long pad_blocks = sa->cnt > 0 ? (krow_count(*sa) + 3) / 4 : 0;
+    if (stage_blocks + rw_blocks + pad_blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(front_kernel, dim3((unsigned)(stage_blocks + rw_blocks + pad_blocks)), dim3(NT), 0,
+                       (hipStream_t)stream, *ra, *sa, (unsigned)stage_blocks, (unsigned)kblocks, (unsigned)rw_blocks);
     return (int)hipGetLastError();
 }
 

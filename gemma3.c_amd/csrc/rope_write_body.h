@@ -15,6 +15,43 @@ __device__ __forceinline__ uint32_t pack_f16(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | (uint32_t)__builtin_bit_cast(uint16_t, b) << 16;
 }
 
+// One staged key row (1 KiB: row points at its fp16 hi half) from this
+// lane's four dims {2l, 2l+1} (x0, x1) and {2l+128, 2l+129} (x2, x3); the
+// wave holds the whole 256-float row.  scale == nullptr: the exact format,
+// fp16 hi | fp16 lo.  Otherwise the fp8 cross format of G3K_KROW_X8 (fp16 hi
+// | e4m3 of hi / 2^E and of lo * 2^11 / 2^E) and the row's E8M0 scale byte
+// 127 + E, written by lane 0.
+__device__ __forceinline__ void write_krow(uint16_t *row, uint8_t *scale, float x0, float x1, float x2, float x3,
+                                           int lane) {
+    constexpr int D = G3K_HEAD_DIM;
+    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1, h2 = (_Float16)x2, h3 = (_Float16)x3;
+    const float l0 = x0 - (float)h0, l1 = x1 - (float)h1, l2 = x2 - (float)h2, l3 = x3 - (float)h3;
+    *reinterpret_cast<uint32_t *>(row + 2 * lane) = pack_f16(h0, h1);
+    *reinterpret_cast<uint32_t *>(row + 128 + 2 * lane) = pack_f16(h2, h3);
+    if (!scale) {
+        *reinterpret_cast<uint32_t *>(row + D + 2 * lane) = pack_f16((_Float16)l0, (_Float16)l1);
+        *reinterpret_cast<uint32_t *>(row + D + 128 + 2 * lane) = pack_f16((_Float16)l2, (_Float16)l3);
+        return;
+    }
+    const float m = wave_max(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))));
+    const int E = x8_exponent(m);
+    const float inv = __builtin_amdgcn_ldexpf(1.0f, -E), inv_lo = __builtin_amdgcn_ldexpf(1.0f, 11 - E);
+    unsigned char *x8 = reinterpret_cast<unsigned char *>(row);
+    // dims 2l, 2l+1 and 2l+128, 2l+129 are adjacent bytes of one 8-byte run
+    // (u even, u + 1), so each pair is one 16-bit store per part
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int d = 2 * lane + 128 * k;
+        const int t = d >> 5, g = (d >> 3) & 3, u = d & 7;
+        const int off = 512 + 64 * (t >> 1) + 16 * g + 8 * (t & 1) + u;
+        const float ha = (float)(k ? h2 : h0), hb = (float)(k ? h3 : h1);
+        const float la = k ? l2 : l0, lb = k ? l3 : l1;
+        *reinterpret_cast<uint16_t *>(x8 + off) = (uint16_t)e4m3_pair(ha * inv, hb * inv);
+        *reinterpret_cast<uint16_t *>(x8 + off + 256) = (uint16_t)e4m3_pair(la * inv_lo, lb * inv_lo);
+    }
+    if (lane == 0) *scale = (uint8_t)(127 + E);
+}
+
 // Wave wid of the batch (token wid / nvec, vector wid % nvec: the Q heads,
 // then K, then V); lane l holds dims {2l, 2l+1} and their RoPE partners
 // {2l+128, 2l+129}.
@@ -65,15 +102,9 @@ __device__ __forceinline__ void rope_write_vec(const g3k_rope_write_args &a, lon
     }
 
     if (kind == 1 && a.kq) {
-        // prefill staging: fp16 hi | lo row of the rotated key
-        const _Float16 h0 = (_Float16)lo.x, h1 = (_Float16)lo.y, h2 = (_Float16)hi.x, h3 = (_Float16)hi.y;
-        const _Float16 l0 = (_Float16)(lo.x - (float)h0), l1 = (_Float16)(lo.y - (float)h1);
-        const _Float16 l2 = (_Float16)(hi.x - (float)h2), l3 = (_Float16)(hi.y - (float)h3);
-        uint16_t *row = a.kq + ((size_t)h * a.ldk + a.row0 + i) * (2 * D);
-        *reinterpret_cast<uint32_t *>(row + 2 * lane) = pack_f16(h0, h1);
-        *reinterpret_cast<uint32_t *>(row + 128 + 2 * lane) = pack_f16(h2, h3);
-        *reinterpret_cast<uint32_t *>(row + D + 2 * lane) = pack_f16(l0, l1);
-        *reinterpret_cast<uint32_t *>(row + D + 128 + 2 * lane) = pack_f16(l2, l3);
+        // prefill staging: the rotated key's row in the staging format
+        const size_t r = (size_t)h * a.ldk + a.row0 + i;
+        write_krow(a.kq + r * (2 * D), a.kscale ? a.kscale + r : nullptr, lo.x, lo.y, hi.x, hi.y, lane);
     }
     if (kind != 0 && i < a.kv_skip) return;
 

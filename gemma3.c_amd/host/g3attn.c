@@ -148,6 +148,8 @@ struct g3attn_ctx {
     int min_rows;   /* smallest heuristic split */
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
     int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
+    int prefill_x8;    /* prefill scores: 1 = fp16 hi + fp8 cross terms (default), 0 = three
+                        * fp16 passes (G3ATTN_PREFILL_QK=exact) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
     int n_cu;       /* compute units of the device */
     /* decode: non-temporal cache loads on 1 every layer, 2 global layers
@@ -322,6 +324,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         c->prefill_qpw = (qpw && atoi(qpw) == 32) ? 32 : 16;
         const char *sch = getenv("G3ATTN_PREFILL_SCHED");
         c->prefill_sched = sch ? atoi(sch) : 1;
+        const char *qk = getenv("G3ATTN_PREFILL_QK");
+        c->prefill_x8 = !(qk && strcmp(qk, "exact") == 0);
         const char *nt = getenv("G3ATTN_DECODE_NT");
         c->nt_loads = nt ? atoi(nt) : 2;
         const char *ff = getenv("G3ATTN_FORWARD_FOLD");
@@ -827,9 +831,21 @@ static int prefill_splits(int n, int hist, int nk, int window, int pb, int n_kv,
     return best;
 }
 
+/* x8: the score policy, 1 = fp16 hi + fp8 cross terms, 0 = three fp16
+ * passes (see prefill.hip). */
+static int prefill_attention(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q, const float *K,
+                             const float *V, const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out,
+                             int x8);
+
 int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q,
                           const float *K, const float *V, const uint16_t *q_norm,
                           const uint16_t *k_norm, float *attn_out) {
+    return prefill_attention(c, layer, start_pos, n, Q, K, V, q_norm, k_norm, attn_out, c ? c->prefill_x8 : 0);
+}
+
+static int prefill_attention(g3attn_ctx *c, int layer, int start_pos, int n, const float *Q, const float *K,
+                             const float *V, const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out,
+                             int x8) {
     if (!check_layer(c, layer, "g3attn_prefill") || !check_rope(c, "g3attn_prefill")) return G3_ERR_INVALID_ARG;
     if (n < 0 || start_pos < 0 || (n > 0 && (!Q || !K || !V || !attn_out))) {
         set_err("g3attn_prefill: null buffer or negative start_pos / n");
@@ -855,15 +871,18 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     const int S = prefill_splits(n, hist, nk, is_global ? INT_MAX / 2 : W, pb, Hkv, Hq, c->n_cu);
     const size_t po_bytes = S > 1 ? align256((size_t)S * n * Hq * D * sizeof(float)) : 0;
     const size_t pml_bytes = S > 1 ? align256((size_t)S * n * Hq * 2 * sizeof(float)) : 0;
+    /* the fp8 cross policy's key-scale bytes, one per staged key row */
+    const size_t ks_bytes = x8 ? align256((size_t)Hkv * ldk) : 0;
     hipSetDevice(c->device);
-    int rc = grow_pf(c, 4 * v_bytes + po_bytes + pml_bytes);
+    int rc = grow_pf(c, 4 * v_bytes + ks_bytes + po_bytes + pml_bytes);
     if (rc) return rc;
     unsigned char *ws = (unsigned char *)c->d_pf;
     uint16_t *kq = (uint16_t *)ws;
     uint16_t *vt = (uint16_t *)(ws + 2 * v_bytes);
     uint16_t *vt_lo = (uint16_t *)(ws + 3 * v_bytes);
-    float *part_o = S > 1 ? (float *)(ws + 4 * v_bytes) : NULL;
-    float *part_ml = S > 1 ? (float *)(ws + 4 * v_bytes + po_bytes) : NULL;
+    uint8_t *kscale = x8 ? ws + 4 * v_bytes : NULL;
+    float *part_o = S > 1 ? (float *)(ws + 4 * v_bytes + ks_bytes) : NULL;
+    float *part_ml = S > 1 ? (float *)(ws + 4 * v_bytes + ks_bytes + po_bytes) : NULL;
     /* a fresh epoch per call: a flag left by an earlier call never matches */
     c->pf_epoch = c->pf_epoch >= INT_MAX - 1 ? 1 : c->pf_epoch + 1;
     const int norm = q_norm && k_norm;
@@ -886,6 +905,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
         sa.nk = nk;
         sa.n_kv_heads = Hkv;
         sa.kq = kq;
+        sa.kscale = kscale;
         sa.vt = vt;
         sa.vt_lo = vt_lo;
         sa.ldk = ldk;
@@ -917,6 +937,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     ra.dst_pos0 = 0;
     ra.kv_skip = (!is_global && n > W) ? n - W : 0;
     ra.kq = kq;
+    ra.kscale = kscale;
     ra.ldk = ldk;
     ra.row0 = hist;
     /* 3. the batch's values as bf16 hi / lo V^T, and zeroed padding up to
@@ -936,6 +957,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
         sa.nk = nk;
         sa.n_kv_heads = Hkv;
         sa.kq = kq;
+        sa.kscale = kscale;
         sa.vt = vt;
         sa.vt_lo = vt_lo;
         sa.ldk = ldk;
@@ -954,6 +976,7 @@ int g3attn_prefill_device(g3attn_ctx *c, int layer, int start_pos, int n, const 
     pa.eps = c->cfg.rmsnorm_eps;
     pa.start_pos = start_pos;
     pa.kq = kq;
+    pa.kscale = kscale;
     pa.vt = vt;
     pa.vt_lo = vt_lo;
     pa.v_lo_flag = c->d_vflag;
@@ -1471,7 +1494,10 @@ static int prefill_chunk(g3attn_ctx *c, const g3attn_weights *w, int n, int pos0
         g.ldc[1] = g.ldc[2] = ks;
         if ((rc = gemm_step(c, &g))) return rc;
         /* QK-norm, RoPE, cache write, attention (:641-692) */
-        if ((rc = g3attn_prefill_device(c, l, pos0, n, b->q, b->k, b->v, lw->q_norm, lw->k_norm, b->attn)))
+        /* the whole-model path keeps the exact score policy: its logits are
+         * held to the token forward's 1e-4 x RMS, tighter than the
+         * attention path's 2e-3 */
+        if ((rc = prefill_attention(c, l, pos0, n, b->q, b->k, b->v, lw->q_norm, lw->k_norm, b->attn, 0)))
             return rc;
         /* o_proj (:694-699) */
         memset(&r, 0, sizeof r);

@@ -119,7 +119,15 @@ int g3attn_decode(g3attn_ctx *ctx, int layer, int pos,
  * K, V [n][num_kv_heads*256] (pre-norm), attn_out [n][num_heads*256].
  * Token i sees exactly the keys the sequential loop gives it: positions
  * [0, pos] (global) or [pos-window+1, pos] (local), including keys cached by
- * earlier calls when start_pos > 0.  Blocking. */
+ * earlier calls when start_pos > 0.  Blocking.
+ * Scores use fp16 q_hi k_hi plus the cross terms q_lo k_hi + q_hi k_lo as
+ * scaled fp8 products (per-key and per-query power-of-two scales, so any
+ * input range fp16 holds keeps its precision): about 4e-4 x output RMS
+ * against the reference at the configs, against the path's 2e-3 bar.  The
+ * environment variable G3ATTN_PREFILL_QK=exact, read at g3attn_create,
+ * selects three fp16 passes instead (about 1e-4).  The whole-model batched
+ * prefill (g3attn_prefill_forward_device, g3attn_prefill_tokens) always
+ * uses the exact scores: its logits are held to 1e-4 x RMS. */
 int g3attn_prefill(g3attn_ctx *ctx, int layer, int start_pos, int n,
                    const float *Q, const float *K, const float *V,
                    const uint16_t *q_norm, const uint16_t *k_norm, float *attn_out);

@@ -4,8 +4,11 @@ The oracle restates the reference's sequential per-token prefill loop
 (gemma3_transformer.c:641-692): QK-norm -> RoPE -> cache_kv -> gemma3_gqa
 for each token in order.  Both sides consume the same seeded, bf16-valued
 inputs.  Bar: max-abs error <= 2e-3 x output RMS (the north-star tolerance
-for the bf16/fp16-MFMA path).  The kernel's split-precision policy lands
-near 1e-5, so a regression to single-pass precision fails loudly.
+for the bf16/fp16-MFMA path).  The default score policy (fp16 q_hi k_hi plus
+the cross terms as scaled fp8 products) lands near 4e-4 at configs[3] and
+below elsewhere, the exact policy (three fp16 passes, G3ATTN_PREFILL_QK=exact)
+near 1e-4; a single-pass score or P (1e-2 and up on the early causal rows)
+fails loudly.
 
 configs[2] (local, N=2048, window 1024) and configs[3] (global, N=8192) are
 checked in full (every row; the oracle runs 16 threads), configs[3] also
@@ -345,3 +348,25 @@ def test_split_merge_repeats_in_one_context(ctx8k):
                 first.append(got)
             else:
                 assert np.array_equal(got, first[i]), (rep, i)
+
+
+def test_exact_score_policy(monkeypatch):
+    """G3ATTN_PREFILL_QK=exact (three fp16 score passes, the key rows staged
+    fp16 hi | lo) on the forms cases: each within 5e-4 x RMS of the oracle
+    (it lands near 1e-4), and different from the default fp8 cross policy's
+    output, which is itself within the bar (so the switch takes effect)."""
+    for kw, cases in _forms_cases():
+        with _ctx(**kw) as c:
+            default = [case.gpu(c) for _, case in cases]
+        monkeypatch.setenv("G3ATTN_PREFILL_QK", "exact")
+        with _ctx(**kw) as c:
+            for (name, case), x8 in zip(cases, default):
+                got = case.gpu(c)
+                want, Kc, Vc = case.oracle()
+                err, err_x8 = rel_err(got, want), rel_err(x8, want)
+                print(f"[exact policy {name}] rel_err={err:.3e} (fp8 cross policy {err_x8:.3e})", flush=True)
+                assert err <= 5e-4, (name, err)
+                assert err_x8 <= TOL, (name, err_x8)
+                _check_cache(c, case, Kc, Vc)
+                assert not np.array_equal(got, x8), name
+        monkeypatch.delenv("G3ATTN_PREFILL_QK")

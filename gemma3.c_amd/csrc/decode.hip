@@ -553,6 +553,123 @@ extern "C" int g3k_noalloc_scratch(float **acc, float **ml) {
     return 0;
 }
 
+// ---------------------------------------------------------------------------
+// gemma3_gqa of any shape (the fast kernels above take head_dim 256 and
+// groups 1, 2, 4).  One workgroup per (split, query head), 256 threads: each
+// 16-lane group takes one key row per step (lane c holds dims c + 16 j), so
+// a wave scores four rows at once and reduces each dot product with four DPP
+// adds; every lane group keeps its own online softmax over its rows.  The
+// 16 lane groups of the workgroup then merge through LDS, per dim.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int GEN_J = G3K_GQA_MAX_DIM / 16;   // dims per lane, at most
+
+__global__ __launch_bounds__(NT) void gqa_generic_kernel(g3k_gqa_args a) {
+    __shared__ float s_acc[16][G3K_GQA_MAX_DIM];
+    __shared__ float s_m[16], s_l[16];
+    const int split = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, grp = tid >> 4, c = tid & 15;   // 16 lane groups of the workgroup
+    const int hd = a.head_dim;
+    const int kvh = h / (a.n_heads / a.n_kv_heads);
+    const long long rs = (long long)a.n_kv_heads * hd;
+    float qv[GEN_J], acc[GEN_J];
+#pragma unroll
+    for (int j = 0; j < GEN_J; j++) {
+        const int d = c + 16 * j;
+        qv[j] = d < hd ? a.q[(size_t)h * hd + d] * a.qscale : 0.f;
+        acc[j] = 0.f;
+    }
+    float m = NEG_BIG, l = 0.f;
+    const int c0 = split * a.rows_per_split, c1 = min(c0 + a.rows_per_split, a.seq_len);
+    // wave-uniform trip count (the DPP reduction needs every lane of the
+    // wave); a lane group past the split's end scores -inf and adds nothing
+    for (int base = c0; base < c1; base += 16) {
+        const int row = base + grp;
+        const bool valid = row < c1;
+        const int r = valid ? row : c0;
+        const float *kr = a.k + (size_t)r * rs + (size_t)kvh * hd;
+        const float *vr = a.v + (size_t)r * rs + (size_t)kvh * hd;
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < GEN_J; j++) {
+            const int d = c + 16 * j;
+            if (d < hd) dot += qv[j] * kr[d];
+        }
+        float sc = row16_sum(dot);
+        if (a.mask) sc += a.mask[r] * 1.4426950408889634f;
+        sc = valid ? sc : -INFINITY;
+        const float mn = fmaxf(m, sc);
+        const float alpha = fast_exp2(m - mn), pr = fast_exp2(sc - mn);
+        m = mn;
+        l = l * alpha + pr;
+#pragma unroll
+        for (int j = 0; j < GEN_J; j++) {
+            const int d = c + 16 * j;
+            acc[j] = acc[j] * alpha + (d < hd ? pr * vr[d] : 0.f);
+        }
+    }
+    // lane groups whose rows were all masked to -inf keep m = -inf: their
+    // weight below is exp2(-inf - M) = 0 (M is finite when any row is)
+#pragma unroll
+    for (int j = 0; j < GEN_J; j++) {
+        const int d = c + 16 * j;
+        if (d < hd) s_acc[grp][d] = acc[j];
+    }
+    if (c == 0) {
+        s_m[grp] = m;
+        s_l[grp] = l;
+    }
+    __syncthreads();
+    float M = s_m[0];
+    for (int g = 1; g < 16; g++) M = fmaxf(M, s_m[g]);
+    float L = 0.f;
+    for (int g = 0; g < 16; g++) L += s_l[g] * fast_exp2(s_m[g] - M);
+    const size_t slot = (size_t)h * a.n_splits + split;
+    for (int d = tid; d < hd; d += NT) {
+        float A = 0.f;
+        for (int g = 0; g < 16; g++) A += s_acc[g][d] * fast_exp2(s_m[g] - M);
+        if (a.n_splits == 1)
+            a.out[(size_t)h * hd + d] = A / L;
+        else
+            a.ws_acc[slot * hd + d] = A;
+    }
+    if (a.n_splits > 1 && tid == 0) {
+        a.ws_ml[slot * 2] = M;
+        a.ws_ml[slot * 2 + 1] = L;
+    }
+}
+
+// The splits' partials of one query head, merged in split order per dim.
+__global__ __launch_bounds__(NT) void gqa_generic_combine_kernel(g3k_gqa_args a) {
+    const int h = blockIdx.x, hd = a.head_dim, S = a.n_splits;
+    const size_t s0 = (size_t)h * S;
+    float M = NEG_BIG;
+    for (int s = 0; s < S; s++) M = fmaxf(M, a.ws_ml[(s0 + s) * 2]);
+    float L = 0.f;
+    for (int s = 0; s < S; s++) L += a.ws_ml[(s0 + s) * 2 + 1] * fast_exp2(a.ws_ml[(s0 + s) * 2] - M);
+    for (int d = threadIdx.x; d < hd; d += NT) {
+        float A = 0.f;
+        for (int s = 0; s < S; s++) A += a.ws_acc[(s0 + s) * hd + d] * fast_exp2(a.ws_ml[(s0 + s) * 2] - M);
+        a.out[(size_t)h * hd + d] = A / L;
+    }
+}
+
+}  // namespace
+
+extern "C" int g3k_gqa_generic(const g3k_gqa_args *a, void *stream) {
+    if (a->n_heads < 1 || a->n_kv_heads < 1 || a->n_heads % a->n_kv_heads || a->seq_len < 1 ||
+        a->head_dim < 1 || a->head_dim > G3K_GQA_MAX_DIM || a->n_splits < 1 || a->rows_per_split < 1 ||
+        (long long)a->n_splits * a->rows_per_split < a->seq_len || (a->n_splits > 1 && (!a->ws_acc || !a->ws_ml)))
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(gqa_generic_kernel, dim3(a->n_splits, a->n_heads), dim3(NT), 0, st, *a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a->n_splits == 1) return (int)e;
+    hipLaunchKernelGGL(gqa_generic_combine_kernel, dim3(a->n_heads), dim3(NT), 0, st, *a);
+    return (int)hipGetLastError();
+}
+
 extern "C" int g3k_decode_capacity(int group, int fused) {
     switch (group) {
         case 1: return fused ? capacity<1, true>() : capacity<1, false>();

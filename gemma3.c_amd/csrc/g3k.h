@@ -70,6 +70,23 @@ int g3k_decode_capacity(int group, int fused);
 #define G3K_NOALLOC_MAX_HEADS 16
 int g3k_noalloc_scratch(float **acc, float **ml);
 
+/* gemma3_gqa of any shape the reference computes (gemma3_kernels.c:527-597):
+ * q [n_heads][head_dim] final, k / v rows [seq_len][n_kv_heads][head_dim],
+ * optional additive mask [seq_len], out [n_heads][head_dim]; query head h
+ * reads KV head h / (n_heads / n_kv_heads).  head_dim 1..G3K_GQA_MAX_DIM,
+ * any group.  Split-K over n_splits runs of rows_per_split keys; with more
+ * than one split the partials go to ws_acc [n_heads][n_splits][head_dim] and
+ * ws_ml [n_heads][n_splits][2] and a second launch merges them. */
+#define G3K_GQA_MAX_DIM 512
+typedef struct {
+    const float *q, *k, *v, *mask;
+    float *out, *ws_acc, *ws_ml;
+    int n_heads, n_kv_heads, seq_len, head_dim;
+    int n_splits, rows_per_split;
+    float qscale;          /* softmax scale * log2(e) */
+} g3k_gqa_args;
+int g3k_gqa_generic(const g3k_gqa_args *a, void *stream);
+
 /* Batched QK-norm + RoPE + cache write for n tokens (positions start_pos..).
  *   Q [n][H_q][D] (may be NULL) -> q_out head-major [H_q][n][D];
  *   K, V [n][H_kv][D] -> k_dst/v_dst rows: slot = ring ? (pos % ring) : (pos - dst_pos0),

@@ -74,6 +74,9 @@ constexpr float LAZY = 8.0f;                 // log2 headroom of the lazy max
 #ifndef G3K_KPF
 #define G3K_KPF 1                            // K fragment prefetch depth (d-steps)
 #endif
+#ifndef G3K_VPF
+#define G3K_VPF 2                            // V^T fragment prefetch depth (16-dim blocks)
+#endif
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -638,12 +641,12 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
         auto softmax_pv = [&]() {
           if (wave_live && kt >= wkt0 && kt <= wkt1) {
             // the first V^T fragments load while the softmax runs
-            bf16x8 vf[3], vl[3];
-            vf[0] = *reinterpret_cast<const bf16x8 *>(vs + voff);
-            vf[1] = *reinterpret_cast<const bf16x8 *>(vs + voff + 1024);
-            if (VLO) {
-                vl[0] = *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff);
-                vl[1] = *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff + 1024);
+            constexpr int VPF = G3K_VPF;
+            bf16x8 vf[VPF + 1], vl[VPF + 1];
+#pragma unroll
+            for (int i = 0; i < VPF; i++) {
+                vf[i] = *reinterpret_cast<const bf16x8 *>(vs + voff + 1024 * i);
+                if (VLO) vl[i] = *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff + 1024 * i);
             }
             const bool edge = (kt * BK + BK - 1 > w_first) || (kt * BK <= w_last - p.window) ||
                               (kt * BK + BK > p.nk);
@@ -688,22 +691,24 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
                 l_sum[b] += psum;   // this lane's keys; the four lanes add up at the end
             }
             // ---- O^T += V^T . P^T over 16 dim blocks; the V^T fragments of
-            // block mt + 2 are read while block mt's MFMAs run ----
+            // block mt + VPF are read while block mt's MFMAs run ----
 #pragma unroll
             for (int mt = 0; mt < 16; mt++) {
-                if (mt + 2 < 16) {
-                    vf[(mt + 2) % 3] = *reinterpret_cast<const bf16x8 *>(vs + voff + 1024 * (mt + 2));
+                if (mt + VPF < 16) {
+                    vf[(mt + VPF) % (VPF + 1)] = *reinterpret_cast<const bf16x8 *>(vs + voff + 1024 * (mt + VPF));
                     if (VLO)
-                        vl[(mt + 2) % 3] =
-                            *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff + 1024 * (mt + 2));
+                        vl[(mt + VPF) % (VPF + 1)] =
+                            *reinterpret_cast<const bf16x8 *>(vs + VTILEB + voff + 1024 * (mt + VPF));
                 }
                 sched_fence();
 #pragma unroll
                 for (int b = 0; b < NQB; b++) {
-                    o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt % 3], ph[b], o[b][mt], 0, 0, 0);
-                    o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[mt % 3], pl[b], o[b][mt], 0, 0, 0);
+                    const bf16x8 v = vf[mt % (VPF + 1)];
+                    o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, ph[b], o[b][mt], 0, 0, 0);
+                    o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, pl[b], o[b][mt], 0, 0, 0);
                     if (VLO)
-                        o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl[mt % 3], ph[b], o[b][mt], 0, 0, 0);
+                        o[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl[mt % (VPF + 1)], ph[b], o[b][mt], 0,
+                                                                          0, 0);
                 }
                 sched_fence();
             }

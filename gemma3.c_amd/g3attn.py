@@ -173,6 +173,9 @@ def gqa(q, k_cache, v_cache, n_heads, n_kv_heads, seq_len, head_dim=256, scale=0
     return out
 
 
+NOALLOC_MAX_HEADS = 16   # G3ATTN_NOALLOC_MAX_HEADS
+
+
 def gqa_noalloc(out_ptr, q_ptr, k_ptr, v_ptr, n_heads, n_kv_heads, seq_len, head_dim=256,
                 scale=0.0625, mask_ptr=None, stream=None) -> None:
     """g3attn_gqa_noalloc on device addresses (ints); enqueues and returns."""

@@ -1956,29 +1956,78 @@ static void gqa_args(g3k_decode_args *a, float *dout, const float *dq, const flo
     a->ws_ml = ws_ml;
 }
 
+/* gemma3_gqa computes any shape whose KV-head index h / (n_heads /
+ * n_kv_heads) stays below n_kv_heads, i.e. n_kv_heads divides n_heads (other
+ * shapes read past the reference's rows); head_dim up to G3K_GQA_MAX_DIM. */
 static int gqa_check(const float *output, const float *q, const float *k_cache, const float *v_cache,
                      int n_heads, int n_kv, int seq_len, int head_dim, const char *who) {
     if (!output || !q || !k_cache || !v_cache || seq_len <= 0) {
         set_err("%s: null buffer or seq_len <= 0", who);
         return G3_ERR_INVALID_ARG;
     }
-    if (!check_shape(n_heads, n_kv, head_dim)) return G3_ERR_INVALID_ARG;
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv) {
+        set_err("%s: num_heads %d not a multiple of num_kv_heads %d", who, n_heads, n_kv);
+        return G3_ERR_INVALID_ARG;
+    }
+    if (head_dim < 1 || head_dim > G3K_GQA_MAX_DIM) {
+        set_err("%s: head_dim %d outside 1..%d", who, head_dim, G3K_GQA_MAX_DIM);
+        return G3_ERR_INVALID_ARG;
+    }
     return G3_OK;
+}
+
+/* The split-K decode kernels take head_dim 256 and groups 1, 2, 4 (the
+ * model's shapes); every other shape goes to the general kernel. */
+static int gqa_fast_shape(int n_heads, int n_kv, int head_dim) {
+    const int g = n_heads / n_kv;
+    return head_dim == D && (g == 1 || g == 2 || g == 4) && n_kv <= GQA_MAX_KV;
+}
+
+/* Split-K shape of the general kernel: about 512 workgroups over the query
+ * heads, at least 32 rows per split, and a workspace of at most max_acc
+ * partial floats ([n_heads][splits][head_dim]). */
+static void gqa_generic_args(g3k_gqa_args *a, float *dout, const float *dq, const float *dk, const float *dv,
+                             const float *dm, int n_heads, int n_kv, int seq_len, int head_dim, float scale,
+                             float *ws_acc, float *ws_ml, size_t max_acc) {
+    memset(a, 0, sizeof *a);
+    int S = (512 + n_heads - 1) / n_heads;
+    const int by_rows = (seq_len + 31) / 32;
+    if (S > by_rows) S = by_rows;
+    if (S > G3K_MAX_SPLITS) S = G3K_MAX_SPLITS;
+    const size_t fit = max_acc / ((size_t)n_heads * head_dim);
+    if ((size_t)S > fit) S = (int)fit;
+    if (S < 1) S = 1;
+    a->rows_per_split = (seq_len + S - 1) / S;
+    a->n_splits = (seq_len + a->rows_per_split - 1) / a->rows_per_split;
+    a->q = dq;
+    a->k = dk;
+    a->v = dv;
+    a->mask = dm;
+    a->out = dout;
+    a->ws_acc = ws_acc;
+    a->ws_ml = ws_ml;
+    a->n_heads = n_heads;
+    a->n_kv_heads = n_kv;
+    a->seq_len = seq_len;
+    a->head_dim = head_dim;
+    a->qscale = scale * LOG2E;
 }
 
 static int gqa_run(float *output, const float *q, const float *k_cache, const float *v_cache,
                    int n_heads, int n_kv, int seq_len, int head_dim, float scale, const float *mask) {
     int rc = gqa_check(output, q, k_cache, v_cache, n_heads, n_kv, seq_len, head_dim, "g3attn_gqa");
     if (rc) return rc;
-    if (n_kv > GQA_MAX_KV) {
-        set_err("g3attn_gqa: n_kv_heads %d > %d", n_kv, GQA_MAX_KV);
-        return G3_ERR_INVALID_ARG;
-    }
+    const int fast = gqa_fast_shape(n_heads, n_kv, head_dim);
     rc = gqa_init();
     if (rc) return rc;
     hipSetDevice(g_gqa.device);
-    const size_t qs = (size_t)n_heads * D, kvb = (size_t)seq_len * n_kv * D * sizeof(float);
-    const size_t need = qs * 4 * 2 + 2 * kvb + (size_t)seq_len * 4 + 256;
+    const size_t qs = (size_t)n_heads * head_dim, kvb = (size_t)seq_len * n_kv * head_dim * sizeof(float);
+    /* the general kernel's split partials follow the inputs (at most 256
+     * splits, so at most n_heads * 256 * (head_dim + 2) floats) */
+    const size_t gen_acc = fast ? 0 : (size_t)n_heads * G3K_MAX_SPLITS * head_dim;
+    const size_t gen_ml = fast ? 0 : (size_t)n_heads * G3K_MAX_SPLITS * 2;
+    const size_t in_bytes = align256(qs * 4 * 2 + 2 * kvb + (size_t)seq_len * 4);
+    const size_t need = in_bytes + (gen_acc + gen_ml) * 4 + 256;
     if (need > g_gqa.cap) {
         hipFree(g_gqa.buf);
         g_gqa.buf = NULL;
@@ -1995,9 +2044,17 @@ static int gqa_run(float *output, const float *q, const float *k_cache, const fl
     HIP_TRY(hipMemcpyAsync(dk, k_cache, kvb, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
     HIP_TRY(hipMemcpyAsync(dv, v_cache, kvb, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
     if (mask) HIP_TRY(hipMemcpyAsync(dm, mask, (size_t)seq_len * 4, hipMemcpyHostToDevice, s), "g3attn_gqa upload");
-    g3k_decode_args a;
-    gqa_args(&a, dout, dq, dk, dv, dm, n_heads, n_kv, seq_len, scale, g_gqa.ws_acc, g_gqa.ws_ml);
-    rc = g3k_decode(&a, 0, s);
+    if (fast) {
+        g3k_decode_args a;
+        gqa_args(&a, dout, dq, dk, dv, dm, n_heads, n_kv, seq_len, scale, g_gqa.ws_acc, g_gqa.ws_ml);
+        rc = g3k_decode(&a, 0, s);
+    } else {
+        g3k_gqa_args a;
+        float *acc = (float *)(b + in_bytes);
+        gqa_generic_args(&a, dout, dq, dk, dv, dm, n_heads, n_kv, seq_len, head_dim, scale, acc, acc + gen_acc,
+                         gen_acc);
+        rc = g3k_gqa_generic(&a, s);
+    }
     if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa launch");
     HIP_TRY(hipMemcpyAsync(output, dout, qs * 4, hipMemcpyDeviceToHost, s), "g3attn_gqa download");
     HIP_TRY(hipStreamSynchronize(s), "g3attn_gqa");
@@ -2033,9 +2090,19 @@ int g3attn_gqa_noalloc(float *output, const float *q, const float *k_cache, cons
     float *acc = NULL, *ml = NULL;
     rc = g3k_noalloc_scratch(&acc, &ml);
     if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa_noalloc scratch");
-    g3k_decode_args a;
-    gqa_args(&a, output, q, k_cache, v_cache, mask, n_heads, n_kv_heads, seq_len, scale, acc, ml);
-    rc = g3k_decode(&a, 0, stream);
+    if (gqa_fast_shape(n_heads, n_kv_heads, head_dim)) {
+        g3k_decode_args a;
+        gqa_args(&a, output, q, k_cache, v_cache, mask, n_heads, n_kv_heads, seq_len, scale, acc, ml);
+        rc = g3k_decode(&a, 0, stream);
+    } else {
+        /* the same scratch, in the general kernel's layout: its splits are
+         * capped so the partials fit (n_heads <= 16 and head_dim <= 512 leave
+         * at least 128 splits) */
+        g3k_gqa_args a;
+        gqa_generic_args(&a, output, q, k_cache, v_cache, mask, n_heads, n_kv_heads, seq_len, head_dim, scale, acc,
+                         ml, (size_t)G3K_NOALLOC_MAX_HEADS * G3K_MAX_SPLITS * D);
+        rc = g3k_gqa_generic(&a, stream);
+    }
     if (rc) return hip_fail((hipError_t)rc, "g3attn_gqa_noalloc launch");
     return G3_OK;
 }

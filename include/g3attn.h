@@ -160,11 +160,17 @@ int g3attn_kv_read(g3attn_ctx *ctx, int layer, int slot, int n,
 
 /* Same signature and semantics as gemma3_gqa (gemma3_kernels.h:188-191,
  * gemma3_kernels.c:527-597): q [n_heads][head_dim] (final), k_cache / v_cache
- * [seq_len][n_kv_heads][head_dim], optional additive mask [seq_len];
+ * [seq_len][n_kv_heads][head_dim], optional additive mask [seq_len]; query
+ * head h reads KV head h / (n_heads / n_kv_heads).  Any shape the reference
+ * computes in bounds: n_kv_heads dividing n_heads (any group), head_dim 1 to
+ * 512.  head_dim 256 with groups 1, 2, 4 (the model's shapes) runs the
+ * split-K decode kernels; every other shape a general split-K kernel.
  * scores_buf is accepted and unused.  Host pointers, runs on the default
  * device through a process-wide context; for unit parity and for drop-in use
- * where no cache-owning context exists.  Failures leave output untouched
- * and set g3attn_last_error (the reference also returns silently). */
+ * where no cache-owning context exists (an engine compiled with
+ * -Dgemma3_gqa=g3attn_gqa runs its own attention loop on the GPU this way).
+ * Failures leave output untouched and set g3attn_last_error (the reference
+ * also returns silently). */
 void g3attn_gqa(float *output, const float *q, const float *k_cache, const float *v_cache,
                 int n_heads, int n_kv_heads, int seq_len, int head_dim,
                 float scale, const float *mask, float *scores_buf);
@@ -180,7 +186,8 @@ void g3attn_gqa(float *output, const float *q, const float *k_cache, const float
  * the process ends, so n_heads <= G3ATTN_NOALLOC_MAX_HEADS (larger calls
  * return -1 with a message).  Calls that overlap on one GPU (other streams,
  * other threads) race on that scratch; serialise them.  Same splits and
- * kernels as g3attn_gqa: the results agree bit for bit.  The call enqueues
+ * kernels as g3attn_gqa (the general kernel's splits are capped to fit
+ * the scratch): the results agree bit for bit.  The call enqueues
  * kernel launches only (no allocation, no memset), so it can be recorded into
  * a HIP graph once a first call on the device has run outside capture (that
  * call looks the scratch address up).  Returns 0 or -1. */

@@ -338,8 +338,24 @@ LAYER_TENSORS = ("input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_n
                  "pre_feedforward_layernorm", "post_feedforward_layernorm")
 
 
+GQA_ENGINE_SO = os.path.join(HERE, "_ref", "libg3gqa.so")
+_gqa_engine = None
+
+
+def gqa_engine():
+    """The reference harness compiled with -Dgemma3_gqa=g3attn_gqa
+    (oracle/_ref/libg3gqa.so): the engine's attention on the GPU through the
+    drop-in.  Raises if not built here."""
+    global _gqa_engine
+    if _gqa_engine is None:
+        if not os.path.exists(GQA_ENGINE_SO):
+            raise RuntimeError(f"drop-in engine harness not built: {GQA_ENGINE_SO}")
+        _gqa_engine = _bind_ref(C.CDLL(GQA_ENGINE_SO))
+    return _gqa_engine
+
+
 def forward_seq(cfg: Config, hidden: int, inter: int, tokens, embed: np.ndarray, layers,
-                norm: np.ndarray, use_ref=False):
+                norm: np.ndarray, use_ref=False, ref_lib=None):
     """gemma3_transformer_forward (gemma3_transformer.c:396-512) for tokens at
     positions 0..n-1 from an empty cache.  ``layers`` is a list of
     cfg.num_layers dicts keyed by LAYER_TENSORS (bf16 uint16 arrays; the
@@ -360,8 +376,8 @@ def forward_seq(cfg: Config, hidden: int, inter: int, tokens, embed: np.ndarray,
                 ptrs[13 * l + j] = a.ctypes.data
     logits = np.empty((tokens.size, vocab), dtype=np.float32)
     hid = np.empty(hidden, dtype=np.float32)
-    if use_ref:
-        rc = ref().ref_forward_seq(logits, hid, tokens, tokens.size, embed, ptrs, norm, vocab,
+    if use_ref or ref_lib is not None:
+        rc = (ref_lib or ref()).ref_forward_seq(logits, hid, tokens, tokens.size, embed, ptrs, norm, vocab,
                                    hidden, inter, cfg.num_layers, cfg.num_heads, cfg.num_kv_heads,
                                    cfg.max_context, cfg.sliding_window)
     else:

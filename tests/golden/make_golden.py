@@ -249,10 +249,14 @@ def norm_bf16(n, seed):
     return (a.view(np.uint32) >> 16).astype(np.uint16)
 
 
-def forward_case(**over):
+def forward_case(heads=8, kv_heads=4, **over):
+    """The forward fixture's model (FORWARD, with overrides); other head
+    counts give a model of the same structure for shape tests (the fixture
+    itself is the default 8 / 4)."""
     f = dict(FORWARD, **over)
     H, I, V, L = f["hidden"], f["inter"], f["vocab"], f["layers"]
-    cfg = O.Config(num_layers=L, max_context=f["max_context"], sliding_window=f["window"])
+    cfg = O.Config(num_layers=L, max_context=f["max_context"], sliding_window=f["window"], num_heads=heads,
+                   num_kv_heads=kv_heads)
     qs, ks = cfg.num_heads * 256, cfg.num_kv_heads * 256
     embed = weights_bf16(V, H, 0xF000)
     layers = []

@@ -17,7 +17,9 @@
 //   prefill_device ...                          (same, device pointers)
 //   decode layer pos q k v q_norm k_norm out
 //   matmul N M K W X C                          (g3attn_matmul_bf16_device)
-//   gqa H Hkv seq q k v mask|- out              (g3attn_gqa, host pointers)
+//   gqa H Hkv seq q k v mask|- out [head_dim]   (g3attn_gqa, host pointers;
+//                                                head_dim 256 if absent, scale
+//                                                1 / sqrt(head_dim))
 //   gqa_noalloc H Hkv seq q k v mask|- out      (device copies, null stream;
 //                                                fails if the call allocates)
 //   matvec M K A x y                            (g3attn_matvec_bf16, host)
@@ -38,6 +40,7 @@
 //
 // At the end it prints "launch <kernel> <launches> <workgroups> <threads> <ms>" for every
 // kernel launched and "attn_emu: ok".
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -259,19 +262,20 @@ int main(int argc, char **argv) {
             hipFree(dC);
             write_bin(cf, C.data(), C.size());
         } else if (cmd == "gqa" || cmd == "gqa_noalloc") {
-            int h, hkv, seq;
+            int h, hkv, seq, hd = (int)D;
             std::string qf, kf, vf, mf, of;
             in >> h >> hkv >> seq >> qf >> kf >> vf >> mf >> of;
             if (!in) die("bad " + cmd + " line");
-            const auto q = read_bin<float>(qf, (size_t)h * D);
-            const auto k = read_bin<float>(kf, (size_t)seq * hkv * D);
-            const auto v = read_bin<float>(vf, (size_t)seq * hkv * D);
+            if (!(in >> hd)) hd = (int)D;   // optional head_dim
+            const auto q = read_bin<float>(qf, (size_t)h * hd);
+            const auto k = read_bin<float>(kf, (size_t)seq * hkv * hd);
+            const auto v = read_bin<float>(vf, (size_t)seq * hkv * hd);
             std::vector<float> mask;
             if (mf != "-") mask = read_bin<float>(mf, (size_t)seq);
-            std::vector<float> out((size_t)h * D, -12345.0f);
-            const float scale = 0.0625f;
+            std::vector<float> out((size_t)h * hd, -12345.0f);
+            const float scale = 1.0f / std::sqrt((float)hd);
             if (cmd == "gqa") {
-                g3attn_gqa(out.data(), q.data(), k.data(), v.data(), h, hkv, seq, (int)D, scale,
+                g3attn_gqa(out.data(), q.data(), k.data(), v.data(), h, hkv, seq, hd, scale,
                            mask.empty() ? nullptr : mask.data(), nullptr);
                 if (out[0] == -12345.0f) check(-1, cmd);   // g3attn_gqa reports failure only by leaving out as is
             } else {
@@ -280,7 +284,7 @@ int main(int argc, char **argv) {
                 // the entry point allocates and frees nothing (its split
                 // partials live in the library's fixed device scratch)
                 const unsigned long long allocs = hostemu_alloc_calls();
-                check(g3attn_gqa_noalloc(dout, dq, dk, dv, h, hkv, seq, (int)D, scale, dm, nullptr), cmd);
+                check(g3attn_gqa_noalloc(dout, dq, dk, dv, h, hkv, seq, hd, scale, dm, nullptr), cmd);
                 if (hostemu_alloc_calls() != allocs) die("gqa_noalloc called an allocating entry point");
                 hipDeviceSynchronize();
                 hipMemcpy(out.data(), dout, out.size() * sizeof(float), hipMemcpyDeviceToHost);

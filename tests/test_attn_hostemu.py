@@ -149,11 +149,12 @@ class Emu:
         bound = (2.0 ** -16 + K * 2.0 ** -24) * (np.abs(X64) @ np.abs(W64).T) + 1e-30
         self.checks.append((files[2], X64 @ W64.T, f"matmul N={N} M={M} K={K} (max err / bound)", bound))
 
-    def gqa(self, h, hkv, seq, masked=False, noalloc=False):
-        """g3attn_gqa / _noalloc against the oracle's gemma3_gqa (1e-4 x RMS)."""
-        q = self.rng.standard_normal(h * D).astype(np.float32)
-        k = self.rng.standard_normal(seq * hkv * D).astype(np.float32)
-        v = self.rng.standard_normal(seq * hkv * D).astype(np.float32)
+    def gqa(self, h, hkv, seq, masked=False, noalloc=False, d=D):
+        """g3attn_gqa / _noalloc against the oracle's gemma3_gqa (1e-4 x RMS),
+        scale 1 / sqrt(d)."""
+        q = self.rng.standard_normal(h * d).astype(np.float32)
+        k = self.rng.standard_normal(seq * hkv * d).astype(np.float32)
+        v = self.rng.standard_normal(seq * hkv * d).astype(np.float32)
         files = [self._name(s) for s in ("gq", "gk", "gv", "go")]
         for f, a in zip(files, (q, k, v)):
             self._save(f, a)
@@ -164,9 +165,9 @@ class Emu:
             mf = self._name("gm")
             self._save(mf, mask)
         cmd = "gqa_noalloc" if noalloc else "gqa"
-        self.lines.append(f"{cmd} {h} {hkv} {seq} {files[0]} {files[1]} {files[2]} {mf} {files[3]}")
-        want = O.gqa(q, k, v, h, hkv, seq, mask=mask)
-        self.checks.append((files[3], want, f"{cmd} {h}/{hkv} seq={seq} mask={masked}", 1e-4))
+        self.lines.append(f"{cmd} {h} {hkv} {seq} {files[0]} {files[1]} {files[2]} {mf} {files[3]} {d}")
+        want = O.gqa(q, k, v, h, hkv, seq, d=d, scale=float(np.float32(1.0) / np.sqrt(np.float32(d))), mask=mask)
+        self.checks.append((files[3], want, f"{cmd} {h}/{hkv} d={d} seq={seq} mask={masked}", 1e-4))
 
     def matvec(self, M, K, device=False):
         """g3attn_matvec_bf16 (host) / _device against gemma3_matvec_bf16 (1e-5 x RMS)."""
@@ -375,6 +376,21 @@ def test_gqa_entry_points(built, tmp_path, heads, kv_heads):
     e.gqa(heads, kv_heads, 300, masked=True, noalloc=True)
     e.gqa(heads, kv_heads, 40, noalloc=True)
     e.run()
+
+
+@pytest.mark.parametrize("heads,kv_heads,d", [(6, 2, 64), (3, 1, 96), (8, 1, 512), (2, 2, 40), (5, 5, 1)])
+def test_gqa_general_shapes(built, tmp_path, heads, kv_heads, d):
+    """g3attn_gqa and g3attn_gqa_noalloc on shapes outside the model's
+    (head_dim other than 256, groups other than 1 / 2 / 4): the general
+    split-K kernel, with and without a mask, one split and many, against the
+    oracle's gemma3_gqa."""
+    e = Emu(tmp_path, H=8, Hkv=4)
+    e.gqa(heads, kv_heads, 300, d=d)
+    e.gqa(heads, kv_heads, 20, masked=True, d=d)
+    e.gqa(heads, kv_heads, 700, masked=True, noalloc=True, d=d)
+    e.gqa(heads, kv_heads, 9, noalloc=True, d=d)
+    launches = e.run()
+    assert launches["gqa_generic_kernel"][0] == 4, launches
 
 
 def test_matvec_entry_points(built, tmp_path):

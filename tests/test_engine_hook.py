@@ -182,3 +182,21 @@ def test_engine_returns_a_forward_failure(monkeypatch):
     assert on_gpu == 1 and rc == -1
     rc, on_gpu, _ = run_engine(n_prefill=0)
     assert on_gpu == 1 and rc == -1
+
+
+@pytest.mark.skipif(not os.path.exists(O.GQA_ENGINE_SO), reason="oracle/_ref/libg3gqa.so not built")
+def test_engine_attention_call_is_the_dropin():
+    """oracle/_ref/libg3gqa.so (the engine compiled with
+    -Dgemma3_gqa=g3attn_gqa) resolves its attention call to libg3attn: with no
+    device visible, the engine's gemma3_gqa call (through the harness's
+    ref_gqa) leaves the output untouched and libg3attn reports the missing
+    device, where the CPU reference would have computed it."""
+    if C.CDLL(BACKEND_SO).gemma3_metal_available():
+        pytest.skip("the backend library sees a HIP device")
+    eng = O.gqa_engine()
+    q = np.ones(8 * 256, np.float32)
+    k = v = np.ones(4 * 4 * 256, np.float32)
+    out = np.full(8 * 256, np.nan, np.float32)
+    eng.ref_gqa(out, q, k, v, 8, 4, 4, 256, 0.0625, None, None)
+    assert np.isnan(out).all()
+    assert "device" in g3attn().last_error()

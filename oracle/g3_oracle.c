@@ -504,13 +504,82 @@ uint64_t g3o_fnv1a64(const void *data, size_t nbytes) {
 
 /* ---------------------------------------------------------------- token forward */
 
-/* gemma3_transformer.c:396-512 with layer_mlp (:362-391), for a sequence of
- * tokens from an empty cache (positions 0..n-1). */
-int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
-                    const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
-                    const g3o_model *m) {
+/* The forward's GEMVs split by rows over a small pool of threads (each row's
+ * summation order is g3o_matvec_bf16's, so the result is the same bits for
+ * any thread count).  Each product is a new generation the workers wait for;
+ * the caller takes part and waits until every worker has done its rows. */
+typedef struct {
+    pthread_mutex_t lock;
+    pthread_cond_t start, done_cv;
+    unsigned gen;
+    int workers, done, quit;
+    float *y;
+    const uint16_t *A;
+    const float *x;
+    int M, K;
+} mv_pool;
+
+typedef struct {
+    mv_pool *p;
+    int idx;
+} mv_arg;
+
+static void mv_rows(mv_pool *p, int idx) {
+    const int parts = p->workers + 1;
+    const int lo = (int)((long long)p->M * idx / parts), hi = (int)((long long)p->M * (idx + 1) / parts);
+    for (int i = lo; i < hi; i++) p->y[i] = matvec_row(p->A + (size_t)i * p->K, p->x, p->K);
+}
+
+static void *mv_worker(void *arg) {
+    mv_arg *a = (mv_arg *)arg;
+    mv_pool *p = a->p;
+    unsigned seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&p->lock);
+        while (p->gen == seen && !p->quit) pthread_cond_wait(&p->start, &p->lock);
+        if (p->quit) {
+            pthread_mutex_unlock(&p->lock);
+            return NULL;
+        }
+        seen = p->gen;
+        pthread_mutex_unlock(&p->lock);
+        mv_rows(p, a->idx);
+        pthread_mutex_lock(&p->lock);
+        if (++p->done == p->workers) pthread_cond_signal(&p->done_cv);
+        pthread_mutex_unlock(&p->lock);
+    }
+}
+
+static void pool_matvec(mv_pool *p, float *y, const uint16_t *A, const float *x, int M, int K) {
+    if (!p || p->workers == 0) {
+        g3o_matvec_bf16(y, A, x, M, K);
+        return;
+    }
+    pthread_mutex_lock(&p->lock);
+    p->y = y;
+    p->A = A;
+    p->x = x;
+    p->M = M;
+    p->K = K;
+    p->done = 0;
+    p->gen++;
+    pthread_cond_broadcast(&p->start);
+    pthread_mutex_unlock(&p->lock);
+    mv_rows(p, 0);
+    pthread_mutex_lock(&p->lock);
+    while (p->done < p->workers) pthread_cond_wait(&p->done_cv, &p->lock);
+    pthread_mutex_unlock(&p->lock);
+}
+
+/* gemma3_transformer.c:396-512 with layer_mlp (:362-391): tokens[0..n-1] at
+ * positions pos0.. on caller-owned caches (kc / vc [layer], the reference
+ * layout, updated as cache_kv does); logits for the last n_logits tokens. */
+int g3o_forward_cached(float *logits, int n_logits, float *hidden_last, const int *tokens, int n, int pos0,
+                       const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                       const g3o_model *m, float *const *kc, float *const *vc, int threads) {
     const int H = m->hidden_size, I = m->intermediate_size, V = m->vocab_size, L = m->num_layers;
     const int d = m->head_dim, qs = m->num_heads * d, ks = m->num_kv_heads * d;
+    if (n < 1 || n_logits < 0 || n_logits > n || pos0 < 0 || pos0 + n > m->max_context) return -1;
     g3o_config cfg;
     cfg.num_layers = L;
     cfg.num_heads = m->num_heads;
@@ -528,10 +597,96 @@ int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
     float *gate = malloc((size_t)I * 4), *up = malloc((size_t)I * 4);
     float *work = malloc((size_t)2 * cap * 4);
     float *rl = malloc((size_t)m->max_context * d * 4), *rg = malloc((size_t)m->max_context * d * 4);
+    mv_pool pool;
+    mv_arg args[64];
+    pthread_t tid[64];
+    int pool_on = 0;
+    int rc = 0;
+    if (!x || !xn || !proj || !mlp || !q || !k || !v || !attn || !gate || !up || !work || !rl || !rg) {
+        rc = -4;
+        goto done;
+    }
+    if (threads > 64) threads = 64;
+    if (threads > 1) {
+        /* as many workers as start (fewer threads change no result) */
+        pthread_mutex_init(&pool.lock, NULL);
+        pthread_cond_init(&pool.start, NULL);
+        pthread_cond_init(&pool.done_cv, NULL);
+        pool.gen = 0;
+        pool.workers = 0;
+        pool.done = 0;
+        pool.quit = 0;
+        pool_on = 1;
+        for (int t = 1; t < threads; t++) {
+            args[t].p = &pool;
+            args[t].idx = t;
+            if (pthread_create(&tid[t], NULL, mv_worker, &args[t]) != 0) break;
+            pool.workers++;
+        }
+    }
+    g3o_rope_precompute(rl, m->max_context, d, m->rope_theta_local);
+    g3o_rope_precompute(rg, m->max_context, d, m->rope_theta_global);
+    mv_pool *pp = pool_on ? &pool : NULL;
+    const float escale = sqrtf((float)H);
+    for (int i = 0; i < n && !rc; i++) {
+        const int pos = pos0 + i;
+        for (int j = 0; j < H; j++) x[j] = g3o_bf16_to_f32(embed[(size_t)tokens[i] * H + j]) * escale;
+        for (int l = 0; l < L && !rc; l++) {
+            const uint16_t *const *t = layer_w + (size_t)l * 13;
+            g3o_rmsnorm_bf16(xn, x, t[0], H, m->rmsnorm_eps);
+            pool_matvec(pp, q, t[1], xn, qs, H);
+            pool_matvec(pp, k, t[2], xn, ks, H);
+            pool_matvec(pp, v, t[3], xn, ks, H);
+            rc = g3o_layer_decode(attn, q, k, v, t[5], t[6], kc[l], vc[l],
+                                  g3o_is_global_layer(l) ? rg : rl, &cfg, l, pos, work);
+            if (rc) break;
+            pool_matvec(pp, proj, t[4], attn, H, qs);
+            if (t[7]) g3o_rmsnorm_bf16(proj, proj, t[7], H, m->rmsnorm_eps);
+            for (int j = 0; j < H; j++) x[j] = x[j] + proj[j];
+            if (t[11])
+                g3o_rmsnorm_bf16(xn, x, t[11], H, m->rmsnorm_eps);
+            else
+                memcpy(xn, x, (size_t)H * 4);
+            pool_matvec(pp, gate, t[8], xn, I, H);
+            pool_matvec(pp, up, t[9], xn, I, H);
+            g3o_gelu_tanh(gate, I);
+            for (int j = 0; j < I; j++) gate[j] = gate[j] * up[j];
+            pool_matvec(pp, mlp, t[10], gate, H, I);
+            if (t[12]) g3o_rmsnorm_bf16(mlp, mlp, t[12], H, m->rmsnorm_eps);
+            for (int j = 0; j < H; j++) x[j] = x[j] + mlp[j];
+        }
+        if (rc) break;
+        if (i >= n - n_logits) {
+            g3o_rmsnorm_bf16(xn, x, norm, H, m->rmsnorm_eps);
+            pool_matvec(pp, logits + (size_t)(i - (n - n_logits)) * V, embed, xn, V, H);
+        }
+    }
+    if (!rc && hidden_last) memcpy(hidden_last, x, (size_t)H * 4);
+done:
+    if (pool_on) {
+        pthread_mutex_lock(&pool.lock);
+        pool.quit = 1;
+        pthread_cond_broadcast(&pool.start);
+        pthread_mutex_unlock(&pool.lock);
+        for (int t = 1; t <= pool.workers; t++) pthread_join(tid[t], NULL);
+        pthread_cond_destroy(&pool.start);
+        pthread_cond_destroy(&pool.done_cv);
+        pthread_mutex_destroy(&pool.lock);
+    }
+    free(x); free(xn); free(proj); free(mlp); free(q); free(k); free(v); free(attn);
+    free(gate); free(up); free(work); free(rl); free(rg);
+    return rc;
+}
+
+/* gemma3_transformer.c:396-512 with layer_mlp (:362-391), for a sequence of
+ * tokens from an empty cache (positions 0..n-1), on one thread. */
+int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
+                    const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                    const g3o_model *m) {
+    const int L = m->num_layers, ks = m->num_kv_heads * m->head_dim;
     float **kc = calloc((size_t)L, sizeof(float *)), **vc = calloc((size_t)L, sizeof(float *));
     int rc = 0;
-    if (!x || !xn || !proj || !mlp || !q || !k || !v || !attn || !gate || !up || !work || !rl || !rg ||
-        !kc || !vc) {
+    if (!kc || !vc) {
         rc = -4;
         goto done;
     }
@@ -544,48 +699,13 @@ int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
             goto done;
         }
     }
-    g3o_rope_precompute(rl, m->max_context, d, m->rope_theta_local);
-    g3o_rope_precompute(rg, m->max_context, d, m->rope_theta_global);
-    const float escale = sqrtf((float)H);
-    for (int i = 0; i < n && !rc; i++) {
-        const int pos = i;
-        for (int j = 0; j < H; j++) x[j] = g3o_bf16_to_f32(embed[(size_t)tokens[i] * H + j]) * escale;
-        for (int l = 0; l < L && !rc; l++) {
-            const uint16_t *const *t = layer_w + (size_t)l * 13;
-            g3o_rmsnorm_bf16(xn, x, t[0], H, m->rmsnorm_eps);
-            g3o_matvec_bf16(q, t[1], xn, qs, H);
-            g3o_matvec_bf16(k, t[2], xn, ks, H);
-            g3o_matvec_bf16(v, t[3], xn, ks, H);
-            rc = g3o_layer_decode(attn, q, k, v, t[5], t[6], kc[l], vc[l],
-                                  g3o_is_global_layer(l) ? rg : rl, &cfg, l, pos, work);
-            if (rc) break;
-            g3o_matvec_bf16(proj, t[4], attn, H, qs);
-            if (t[7]) g3o_rmsnorm_bf16(proj, proj, t[7], H, m->rmsnorm_eps);
-            for (int j = 0; j < H; j++) x[j] = x[j] + proj[j];
-            if (t[11])
-                g3o_rmsnorm_bf16(xn, x, t[11], H, m->rmsnorm_eps);
-            else
-                memcpy(xn, x, (size_t)H * 4);
-            g3o_matvec_bf16(gate, t[8], xn, I, H);
-            g3o_matvec_bf16(up, t[9], xn, I, H);
-            g3o_gelu_tanh(gate, I);
-            for (int j = 0; j < I; j++) gate[j] = gate[j] * up[j];
-            g3o_matvec_bf16(mlp, t[10], gate, H, I);
-            if (t[12]) g3o_rmsnorm_bf16(mlp, mlp, t[12], H, m->rmsnorm_eps);
-            for (int j = 0; j < H; j++) x[j] = x[j] + mlp[j];
-        }
-        if (rc) break;
-        g3o_rmsnorm_bf16(xn, x, norm, H, m->rmsnorm_eps);
-        g3o_matvec_bf16(logits + (size_t)i * V, embed, xn, V, H);
-    }
-    if (!rc) memcpy(hidden_last, x, (size_t)H * 4);
+    rc = g3o_forward_cached(logits, n, hidden_last, tokens, n, 0, embed, layer_w, norm, m, kc, vc, 1);
 done:
     if (kc)
         for (int l = 0; l < L; l++) free(kc[l]);
     if (vc)
         for (int l = 0; l < L; l++) free(vc[l]);
-    free(kc); free(vc);
-    free(x); free(xn); free(proj); free(mlp); free(q); free(k); free(v); free(attn);
-    free(gate); free(up); free(work); free(rl); free(rg);
+    free(kc);
+    free(vc);
     return rc;
 }

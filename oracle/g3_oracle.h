@@ -22,7 +22,7 @@
  *   g3o_is_global_layer / g3o_layer_theta    gemma3.h:347-360
  *   g3o_matvec_bf16                          gemma3_kernels.c:146-238 (AVX2 order)
  *   g3o_gelu_tanh                            gemma3_kernels.c:348-357
- *   g3o_forward_seq                          gemma3_transformer.c:396-512 (+ layer_mlp :362-391)
+ *   g3o_forward_seq, g3o_forward_cached      gemma3_transformer.c:396-512 (+ layer_mlp :362-391)
  *
  * How each function is pinned (tests/test_oracle_*.py):
  *   - against golden vectors written by the real reference sources compiled
@@ -108,6 +108,16 @@ typedef struct {
  * tied-embedding logits.  layer_w: num_layers x 13 tensors in the
  * gemma3_weights_t field order (post-attention, pre- and post-feedforward
  * norms may be NULL).  logits [n][vocab]; hidden_last [hidden]. */
+/* The same forward for tokens[0..n-1] at positions pos0..pos0+n-1 on
+ * caller-owned caches kc / vc [num_layers] (reference layout [rows][kv
+ * heads x head_dim], rows = max_context for global layers, sliding_window
+ * for local ones; updated as cache_kv does), so a step can start from any
+ * cache state.  Logits are computed for the last n_logits tokens only
+ * (logits [n_logits][vocab]); hidden_last may be NULL.  The GEMVs split
+ * their rows over `threads` threads (same bits for any count). */
+int g3o_forward_cached(float *logits, int n_logits, float *hidden_last, const int *tokens, int n, int pos0,
+                       const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
+                       const g3o_model *m, float *const *kc, float *const *vc, int threads);
 int g3o_forward_seq(float *logits, float *hidden_last, const int *tokens, int n,
                     const uint16_t *embed, const uint16_t *const *layer_w, const uint16_t *norm,
                     const g3o_model *m);

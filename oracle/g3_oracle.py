@@ -125,6 +125,9 @@ def lib():
         L.g3o_forward_seq.argtypes = [_f32p, _f32p, _i32p, C.c_int, _u16p, C.c_void_p, _u16p,
                                       C.POINTER(_Model)]
         L.g3o_forward_seq.restype = C.c_int
+        L.g3o_forward_cached.argtypes = [_f32p, C.c_int, C.c_void_p, _i32p, C.c_int, C.c_int, _u16p, C.c_void_p,
+                                         _u16p, C.POINTER(_Model), C.c_void_p, C.c_void_p, C.c_int]
+        L.g3o_forward_cached.restype = C.c_int
         L.g3o_splitmix64.argtypes = [C.c_uint64, C.c_uint64]
         L.g3o_splitmix64.restype = C.c_uint64
         L.g3o_fnv1a64.argtypes = [C.c_void_p, C.c_size_t]
@@ -336,6 +339,46 @@ def gelu_tanh(x: np.ndarray) -> np.ndarray:
 LAYER_TENSORS = ("input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
                  "post_attention_layernorm", "gate_proj", "up_proj", "down_proj",
                  "pre_feedforward_layernorm", "post_feedforward_layernorm")
+
+
+def forward_cached(cfg: Config, hidden: int, inter: int, tokens, pos0: int, embed: np.ndarray, layers,
+                   norm: np.ndarray, kc=None, vc=None, n_logits: int = 1, threads: int = 1):
+    """gemma3_transformer_forward for tokens at positions pos0.. on the given
+    caches (lists of cfg.num_layers float32 arrays [rows][kv heads x 256],
+    the reference layout, updated in place; None: empty caches).  Returns
+    (logits of the last n_logits tokens [n_logits][vocab], hidden state
+    after the last token).  The GEMVs split over `threads` threads (same
+    bits for any count)."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    vocab = embed.size // hidden
+    ks = cfg.num_kv_heads * cfg.head_dim
+    if kc is None:
+        kc = [np.zeros((cfg.cache_rows(l), ks), np.float32) for l in range(cfg.num_layers)]
+        vc = [np.zeros((cfg.cache_rows(l), ks), np.float32) for l in range(cfg.num_layers)]
+    for l in range(cfg.num_layers):
+        assert kc[l].dtype == np.float32 and kc[l].flags.c_contiguous and kc[l].shape == (cfg.cache_rows(l), ks)
+        assert vc[l].dtype == np.float32 and vc[l].flags.c_contiguous and vc[l].shape == kc[l].shape
+    keep = []
+    ptrs = (C.c_void_p * (13 * cfg.num_layers))()
+    for l, lw in enumerate(layers):
+        for j, name in enumerate(LAYER_TENSORS):
+            a = lw.get(name)
+            if a is not None:
+                a = np.ascontiguousarray(a, dtype=np.uint16)
+                keep.append(a)
+                ptrs[13 * l + j] = a.ctypes.data
+    kp = (C.c_void_p * cfg.num_layers)(*[a.ctypes.data for a in kc])
+    vp = (C.c_void_p * cfg.num_layers)(*[a.ctypes.data for a in vc])
+    logits = np.empty((n_logits, vocab), dtype=np.float32)
+    hid = np.empty(hidden, dtype=np.float32)
+    m = _Model(vocab, hidden, inter, cfg.num_layers, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+               cfg.max_context, cfg.sliding_window, cfg.rmsnorm_eps, cfg.rope_theta_local, cfg.rope_theta_global)
+    rc = lib().g3o_forward_cached(logits, n_logits, hid.ctypes.data, tokens, tokens.size, pos0,
+                                  np.ascontiguousarray(embed, np.uint16), ptrs, np.ascontiguousarray(norm, np.uint16),
+                                  C.byref(m), kp, vp, threads)
+    if rc:
+        raise RuntimeError(f"g3o_forward_cached -> {rc}")
+    return logits, hid
 
 
 GQA_ENGINE_SO = os.path.join(HERE, "_ref", "libg3gqa.so")

@@ -7,13 +7,23 @@ random bf16 weights: the shapes the bench measures, checked for values.
   against the oracle's restatement of the same forward (g3o_forward_seq) on
   the same host weights.  fp32 throughout on both sides; the bar is 1e-4 x
   RMS per logits row, as for the small-model golden.
-- Batched prefill (g3attn_prefill_tokens for 2048 tokens: MFMA GEMM
+- Token forward at a long position (pos 1100: the local layers' 1024-row
+  rings are full and the global layers attend 1101 keys) on caches
+  pre-filled through g3attn_kv_write, against the oracle's forward
+  (g3o_forward_cached) on the same cache contents; bar 1e-4 x RMS.
+- Batched prefill (g3attn_prefill_tokens for 192 tokens: MFMA GEMM
   projections + the prefill attention kernel, replacing
-  gemma3_transformer_prefill_batched, :526-787) against the token forward
-  looped over the same 2048 tokens (the engine's non-BLAS prefill,
-  :814-821), then one decode step after each.  The GEMMs take x as bf16 hi +
-  lo (16 significant bits) where the GEMV reads fp32 x; the bar is 1e-3 x
-  RMS of the last logits row, with the measured figure printed.
+  gemma3_transformer_prefill_batched, :526-787) and one decode step after it,
+  against the oracle's sequential forward over the same 193 tokens.  The GEMMs
+  take x as bf16 hi + lo (16 significant bits) where the GEMV reads fp32 x;
+  the bar is 1e-3 x RMS of the logits row, with the measured figure printed.
+- The same batched prefill at 2048 tokens against the token forward looped
+  over the same tokens on the GPU (the engine's non-BLAS prefill, :814-821),
+  then one decode step after each: the bench's shape, beyond what the
+  one-core oracle covers in a test's time.
+
+The oracle's GEMVs split their rows over up to 16 host threads (the same bits
+as one thread).
 
 Weights: bf16 N(0,1) x 2^-6 (norm gains N(0,1) x 2^-3) tiled from a seeded
 pool of 2^24 + 43 values, each tensor from its own offset (the odd pool length
@@ -22,6 +32,8 @@ aligned stride).  Both sides read the same bits.  About 7.8 GB of host and
 device memory.  No torch in the process (the tests drive the library's own
 HIP runtime only).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -36,6 +48,8 @@ MAXCTX = 4096
 
 
 POOL = (1 << 24) + 43
+THREADS = max(1, min(16, os.cpu_count() or 1))
+OCFG = O.Config(num_layers=L, max_context=MAXCTX)
 
 
 @pytest.fixture(scope="module")
@@ -92,6 +106,54 @@ def test_forward_full_shapes_vs_oracle(model):
         print(f"[full forward] token {i} (pos {i}): logits rel_err={err:.3e}", flush=True)
         assert err < 1e-4, (i, err)
     assert np.array_equal(got.argmax(axis=1), want.argmax(axis=1))
+
+
+def test_forward_long_position_vs_oracle(model):
+    """One token at pos 1100 on caches whose rows (every slot of the local
+    rings, positions 0..1099 of the global layers) were written through
+    g3attn_kv_write, against the oracle given the same cache contents."""
+    ctx, embed, layers, norm = model
+    pos = 1100
+    rng = np.random.default_rng(0x1100)
+    ctx.reset()
+    kc, vc = [], []
+    for l in range(L):
+        rows = OCFG.cache_rows(l)
+        n = min(rows, pos)
+        k = np.zeros((rows, KS), np.float32)
+        v = np.zeros((rows, KS), np.float32)
+        k[:n] = rng.standard_normal((n, KS), dtype=np.float32)
+        v[:n] = rng.standard_normal((n, KS), dtype=np.float32)
+        ctx.kv_write(l, 0, k[:n], v[:n])
+        kc.append(k)
+        vc.append(v)
+    token = 123457
+    got = ctx.forward_token(token, pos)
+    print("[full model] gpu forward at pos 1100 done; oracle forward", flush=True)
+    want, _ = O.forward_cached(OCFG, H, I, [token], pos, embed, layers, norm, kc, vc, threads=THREADS)
+    err = rel_err(got, want[0])
+    print(f"[full forward] pos {pos} on a pre-filled cache: logits rel_err={err:.3e}", flush=True)
+    assert err < 1e-4
+    assert int(np.argmax(got)) == int(np.argmax(want[0]))
+
+
+def test_batched_prefill_vs_oracle(model):
+    """g3attn_prefill_tokens over 192 tokens (the batched path) and the
+    decode step after it, against the oracle's sequential forward."""
+    ctx, embed, layers, norm = model
+    n = 192
+    tokens = (np.arange(n + 1, dtype=np.int64) * 104729 % (V - 2) + 2).astype(np.int32)
+    ctx.reset()
+    batched = ctx.prefill_tokens(tokens[:n])
+    batched_next = ctx.forward_token(int(tokens[n]), n)
+    print("[full model] gpu batched prefill done; oracle forward over 193 tokens", flush=True)
+    want, _ = O.forward_cached(OCFG, H, I, tokens, 0, embed, layers, norm, n_logits=2, threads=THREADS)
+    e1, e2 = rel_err(batched, want[0]), rel_err(batched_next, want[1])
+    print(f"[full prefill] N={n} vs oracle: last logits rel_err={e1:.3e}; next decode rel_err={e2:.3e}",
+          flush=True)
+    assert e1 < 1e-3 and e2 < 1e-3
+    assert int(np.argmax(batched)) == int(np.argmax(want[0]))
+    assert int(np.argmax(batched_next)) == int(np.argmax(want[1]))
 
 
 def test_batched_prefill_2048_vs_token_loop(model):

@@ -566,3 +566,26 @@ def test_forward_restatement_equals_reference_build_random():
     a = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm)
     b = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm, use_ref=True)
     assert rel(a[0], b[0]) < 1e-5 and rel(a[1], b[1]) < 1e-5
+
+
+def test_forward_cached_is_the_same_forward():
+    """g3o_forward_cached (the forward from caller-owned caches, GEMV rows over
+    a thread pool) against g3o_forward_seq on the forward fixture's model:
+    one call from empty caches with 4 threads gives the same bits for every
+    token's logits; 40 tokens as 25 + 15 in two calls on the same caches
+    give the same last two logits rows (the cache state carries over, ring
+    wrapped), and the caches hold what the sequential run's cache_kv writes."""
+    MG = _mg()
+    cfg, f, embed, layers, norm, tokens = MG.forward_case()
+    want, hid = O.forward_seq(cfg, f["hidden"], f["inter"], tokens, embed, layers, norm)
+    got, hid2 = O.forward_cached(cfg, f["hidden"], f["inter"], tokens, 0, embed, layers, norm,
+                                 n_logits=len(tokens), threads=4)
+    assert np.array_equal(got, want) and np.array_equal(hid, hid2)
+    ks = cfg.num_kv_heads * 256
+    kc = [np.zeros((cfg.cache_rows(l), ks), np.float32) for l in range(cfg.num_layers)]
+    vc = [np.zeros_like(a) for a in kc]
+    O.forward_cached(cfg, f["hidden"], f["inter"], tokens[:25], 0, embed, layers, norm, kc, vc, threads=3)
+    last, _ = O.forward_cached(cfg, f["hidden"], f["inter"], tokens[25:], 25, embed, layers, norm, kc, vc,
+                               n_logits=2, threads=2)
+    assert np.array_equal(last, want[-2:])
+    assert np.any(kc[0] != 0) and np.any(vc[5][: len(tokens)] != 0)

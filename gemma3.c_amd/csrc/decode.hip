@@ -54,6 +54,9 @@ template <int G> constexpr int rows_for() { return G3K_DECODE_ROWS; }
 #else
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 #endif
+#ifndef G3K_DECODE_DB
+#define G3K_DECODE_DB 1   // double-buffered row steps (see the row loop); 0: single set
+#endif
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
 // in flight per wave, one contiguous row range per split.  Double-buffered
@@ -329,12 +332,44 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         }
     }
 
-    // ---- stream this split's rows: reduce the loaded step, then load the next ----
+    // ---- stream this split's rows ----
+#if G3K_DECODE_DB
+    // Two register sets: the next step's loads are issued before the current
+    // step is reduced, so each wave keeps a step in flight while it computes.
+    // The last step is peeled, so every load in the loop body is
+    // unconditional and the waits before each reduction count exactly the
+    // next step's loads.
+    if (base < c1) {
+        float kk2[R][4][4], vv2[R][4][4];
+        for (;;) {
+            int nb = base + stride;
+            if (nb >= c1) {
+                step_compute<G, R, FUSED>(kk, vv, qv, m, l, acc, base, c1, grp, p.mask);
+                break;
+            }
+            load_step<R, NTL>(kk2, vv2, kbase, vbase, p.row_stride, p.head_stride, nb, c1, p.skip, grp, c);
+            __builtin_amdgcn_sched_barrier(0);   // the loads go out before the reduction
+            step_compute<G, R, FUSED>(kk, vv, qv, m, l, acc, base, c1, grp, p.mask);
+            base = nb;
+            nb = base + stride;
+            if (nb >= c1) {
+                step_compute<G, R, FUSED>(kk2, vv2, qv, m, l, acc, base, c1, grp, p.mask);
+                break;
+            }
+            load_step<R, NTL>(kk, vv, kbase, vbase, p.row_stride, p.head_stride, nb, c1, p.skip, grp, c);
+            __builtin_amdgcn_sched_barrier(0);
+            step_compute<G, R, FUSED>(kk2, vv2, qv, m, l, acc, base, c1, grp, p.mask);
+            base = nb;
+        }
+    }
+#else
+    // reduce the loaded step, then load the next
     while (base < c1) {
         step_compute<G, R, FUSED>(kk, vv, qv, m, l, acc, base, c1, grp, p.mask);
         base += stride;
         if (base < c1) load_step<R, NTL>(kk, vv, kbase, vbase, p.row_stride, p.head_stride, base, c1, p.skip, grp, c);
     }
+#endif
 
     // ---- merge the four lane-groups of each wave (they share m) ----
 #pragma unroll

@@ -24,8 +24,12 @@ decode L=512, 128K global-layer decode, the 34-layer decode stack at
 pos 131071 (reference 29 local / 5 global pattern and the config's literal
 28 / 6), configs[2] local prefill (N=2048, window 1024) and configs[3]
 global prefill (N=8192).  Prefill FLOPs are algorithmic: 4 * H_q * d * P for
-P attended (query, key) pairs; the MFMA kernel issues 2.5x that (three fp16
-passes for QK^T, two bf16 passes for PV), reported as "issued".
+P attended (query, key) pairs.  The MFMA kernel issues 2.5x that in FLOPs:
+for QK^T one fp16 pass and two fp8 cross-term passes (which run at twice the
+fp16 rate), for PV two bf16 passes (three with values off the bf16 grid),
+reported as "issued"; in MFMA-pipe time that is 2x the algorithmic work
+(2.5x with the third PV pass), reported as "frac_of_mfma_peak_issued".  With
+G3ATTN_PREFILL_QK=exact (three fp16 QK^T passes) both are 2.5x (3x).
 
 The rows beyond the attention block, at Gemma3-4B shapes with random bf16
 weights (sections `gemv` and `forward`): one layer's Q/K/V + O projection
@@ -695,7 +699,10 @@ def main():
 
     # ---------------- prefill.  The configs' inputs are
     # bf16-valued; the fp32 line feeds values off the bf16 grid, which takes the
-    # kernel's extra P_hi.V_lo pass (3x instead of 2.5x the algorithmic MFMA work).
+    # kernel's extra P_hi.V_lo pass.  Issued FLOPs: QK^T 3x its half of the
+    # algorithmic work, PV 2x (3x); MFMA-pipe time: QK^T 2x under the default
+    # fp8 cross policy (its two fp8 passes at twice the rate), 3x exact.
+    exact_qk = os.environ.get("G3ATTN_PREFILL_QK") == "exact"
     for name, layer, n, window, steps, f32 in (
             ("prefill_local_N2048_w1024", 0, 2048, 1024, 30, False),
             ("prefill_global_N8192", 5, 8192, 1 << 30, 8, False),
@@ -705,7 +712,9 @@ def main():
         ctx = B.context(8192)
         gen = B.randn_f32 if f32 else B.randn_bf16
         Q, K, V = gen(n, QS), gen(n, KS), gen(n, KS)
-        passes = 3.0 if f32 else 2.5
+        passes = 3.0 if f32 else 2.5                       # issued FLOPs / algorithmic
+        pv = 3.0 if f32 else 2.0
+        pipe = (3.0 if exact_qk else 2.0) / 2 + pv / 2    # MFMA-pipe time / algorithmic at the bf16 rate
         zn16 = torch.zeros(D, dtype=torch.int16, device=B.dev)
         pout = torch.empty(n, QS, device=B.dev, dtype=torch.float32)
         torch.cuda.synchronize()
@@ -729,6 +738,8 @@ def main():
             "issued_MFMA_TFLOP/s_kernel": round(passes * flops / k_s / 1e12, 1),
             "frac_of_bf16_peak_algorithmic": round(flops / k_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             "frac_of_bf16_peak_issued": round(passes * flops / k_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "frac_of_mfma_peak_issued": round(pipe * flops / k_s / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "score_policy": "fp16 x3 (exact)" if exact_qk else "fp16 hi + fp8 cross terms",
         }
         log(f"[bench] {name}: {extra[name]}")
         ctx.close()

@@ -96,6 +96,14 @@ constexpr int CP_SC1 = 16;
 
 __device__ __forceinline__ uint16_t bf16_bits(__bf16 h) { return __builtin_bit_cast(uint16_t, h); }
 
+// Two floats -> bf16 (round to nearest even), a in the low half
+// (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, b2));
+}
+
 // ---------------------------------------------------------------------------
 // Staging: fp32 V rows -> bf16 hi and lo V^T columns (workgroups of 64 keys
 // x 64 dims of one head); fp32 K rows -> key rows in the policy's format
@@ -617,23 +625,26 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
 
     // Software pipeline: iteration kt issues tile kt+1's S^T MFMAs and tile
     // kt's softmax + P.V (in either order, see `late`).
-    f32x4 s[NQB][2];
+    // Two score sets, used in turn (the loop is unrolled by two), so no
+    // iteration copies one into the other.  A set is read only for a tile
+    // the wave scored into it (the same liveness test on both sides).
+    f32x4 sc0[NQB][2], sc1[NQB][2];
+#pragma unroll
+    for (int b = 0; b < NQB; b++) sc1[b][0] = sc1[b][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (wave_live && kt0 >= wkt0 && kt0 <= wkt1)
-        tile_scores<NQB, X8>(s, kbuf(kt0), koff0, koff1, qh, qlo, ksbuf(kt0), krow, sb);
+        tile_scores<NQB, X8>(sc0, kbuf(kt0), koff0, koff1, qh, qlo, ksbuf(kt0), krow, sb);
     // the first iteration refills K tile kt0's slot: every wave must be done
     // reading it
     __syncthreads();
 
-    for (int kt = kt0; kt <= kt1; kt++) {
+    // iteration kt: s holds tile kt's scores, sn receives tile kt + 1's
+    auto step = [&](int kt, f32x4 (&s)[NQB][2], f32x4 (&sn)[NQB][2]) {
         // K of tile kt + 2 replaces K of tile kt (scored last iteration), V
         // of tile kt + 1 replaces V of tile kt - 1
         if (kt + 2 <= kt1) fetch_kt(kt + 2);
         if (kt + 1 <= kt1) fetch_vt(kt + 1);
         const unsigned char *vs = vbuf(kt);
 
-        f32x4 sn[NQB][2];
-#pragma unroll
-        for (int b = 0; b < NQB; b++) sn[b][0] = s[b][0], sn[b][1] = s[b][1];
         auto scores_next = [&]() {
             if (wave_live && kt + 1 >= wkt0 && kt + 1 <= wkt1)
                 tile_scores<NQB, X8>(sn, kbuf(kt + 1), koff0, koff1, qh, qlo, ksbuf(kt + 1), krow, sb);
@@ -667,11 +678,14 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
                     }
                 }
                 // ---- online softmax with a lazy reference max ----
+                // The lane's own eight keys first: the max over the query's
+                // four lanes is needed only when one of them passes the lazy
+                // bound, which the ballot shows as well.
                 float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                                  fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-                mx = col4_max(mx);
-                const bool bump = mx > m_ref[b] + LAZY;
-                if (__builtin_amdgcn_ballot_w64(bump)) {
+                if (__builtin_amdgcn_ballot_w64(mx > m_ref[b] + LAZY)) {
+                    mx = col4_max(mx);
+                    const bool bump = mx > m_ref[b] + LAZY;
                     const float m_new = bump ? mx : m_ref[b];
                     const float alpha = fast_exp2(m_ref[b] - m_new);
                     m_ref[b] = m_new;
@@ -679,16 +693,23 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
 #pragma unroll
                     for (int mt = 0; mt < 16; mt++) o[b][mt] *= alpha;
                 }
-                float psum = 0.f;
+                float pr[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const float pr = fast_exp2(sv[u] - m_ref[b]);   // exp2(-inf) = 0 for masked keys
-                    psum += pr;
-                    const __bf16 hi = (__bf16)pr;
-                    ph[b][u] = hi;
-                    pl[b][u] = (__bf16)(pr - (float)hi);
+                for (int u = 0; u < 8; u++) pr[u] = fast_exp2(sv[u] - m_ref[b]);   // exp2(-inf) = 0 for masked keys
+                // this lane's keys (the four lanes add up at the end), as a tree
+                l_sum[b] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+                // P = hi + lo, two bf16 (round to nearest even) per word: each
+                // pair is converted once, and its hi values come back as floats
+                // by a shift and a mask
+                u32x4 hw, lw;
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t h = bf16_pair(pr[2 * u], pr[2 * u + 1]);
+                    hw[u] = h;
+                    lw[u] = bf16_pair(pr[2 * u] - __uint_as_float(h << 16), pr[2 * u + 1] - __uint_as_float(h & 0xffff0000u));
                 }
-                l_sum[b] += psum;   // this lane's keys; the four lanes add up at the end
+                ph[b] = __builtin_bit_cast(bf16x8, hw);
+                pl[b] = __builtin_bit_cast(bf16x8, lw);
             }
             // ---- O^T += V^T . P^T over 16 dim blocks; the V^T fragments of
             // block mt + VPF are read while block mt's MFMAs run ----
@@ -723,13 +744,15 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
             scores_next();
             softmax_pv();
         }
-#pragma unroll
-        for (int b = 0; b < NQB; b++) s[b][0] = sn[b][0], s[b][1] = sn[b][1];
 
         // K of tile kt + 2 and V of tile kt + 1 must have landed before the
         // barrier (next iteration's scores and P.V)
         wait_fetch_all();
         __syncthreads();
+    };
+    for (int kt = kt0; kt <= kt1; kt += 2) {
+        step(kt, sc0, sc1);
+        if (kt + 1 <= kt1) step(kt + 1, sc1, sc0);
     }
 
     // ---- normalise and write attn_out[token][qhead][dim]; with key splits,

@@ -536,7 +536,10 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     const int split = pair % S;
     const int qb = (int)(gridDim.x / (p.n_kv_heads * S)) - 1 - pair / S;
     const int qhead = kvh * G + wave / WPH;
-    const int tok0 = qb * PB + (wave % WPH) * QW;
+    // uniform, so the wave's query range and tile bounds below stay in
+    // SGPRs (the head and the phase order stay per lane: as uniform values
+    // they made the compiler move the O^T accumulators at every phase join)
+    const int tok0 = qb * PB + (fwave % WPH) * QW;
     const bool wave_live = tok0 < p.n;
     // waves w and w + 4 share a SIMD; with schedule 1 the upper four run each
     // tile's softmax + P.V before the next tile's scores
@@ -664,19 +667,22 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
             bf16x8 ph[NQB], pl[NQB];
 #pragma unroll
             for (int b = 0; b < NQB; b++) {
-                const int q_kk = p.hist + tok0 + 16 * b + ln;   // key index of this lane's query
                 // register u of this lane: key kt*32 + 8 g + u (u < 4: s[b][0][u], else s[b][1][u-4])
-                float sv[8] = {s[b][0][0], s[b][0][1], s[b][0][2], s[b][0][3],
-                               s[b][1][0], s[b][1][1], s[b][1][2], s[b][1][3]};
-                // ---- mask (diagonal, window edge, ragged end) ----
+                // ---- mask (diagonal, window edge, ragged end), in place ----
                 if (edge) {
+                    // the query at key index q_kk sees keys q_kk - window + 1
+                    // .. min(q_kk, nk - 1): here u = lo .. hi
+                    const int q_kk = p.hist + tok0 + 16 * b + ln;
+                    const int base = kt * BK + 8 * g;
+                    const int lo = q_kk - p.window + 1 - base, hi = min(q_kk, p.nk - 1) - base;
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
-                        const int kk = kt * BK + 8 * g + u;
-                        const bool ok = kk <= q_kk && kk > q_kk - p.window && kk < p.nk;
-                        sv[u] = ok ? sv[u] : -INFINITY;
+                        const bool ok = u >= lo && u <= hi;
+                        s[b][u >> 2][u & 3] = ok ? s[b][u >> 2][u & 3] : -INFINITY;
                     }
                 }
+                float sv[8] = {s[b][0][0], s[b][0][1], s[b][0][2], s[b][0][3],
+                               s[b][1][0], s[b][1][1], s[b][1][2], s[b][1][3]};
                 // ---- online softmax with a lazy reference max ----
                 // The lane's own eight keys first: the max over the query's
                 // four lanes is needed only when one of them passes the lazy

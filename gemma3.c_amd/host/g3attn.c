@@ -148,6 +148,8 @@ struct g3attn_ctx {
     int min_rows;   /* smallest heuristic split */
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
     int prefill_sched; /* prefill phase schedule 0 / 1 (G3ATTN_PREFILL_SCHED) */
+    int prefill_ksplit; /* G3ATTN_PREFILL_SPLITS: 1, 2 or 4 key splits for every prefill; 0 = the
+                         * makespan model (prefill_splits) */
     int prefill_x8;    /* prefill scores: 1 = fp16 hi + fp8 cross terms (default), 0 = three
                         * fp16 passes (G3ATTN_PREFILL_QK=exact) */
     int target_wgs; /* decode workgroups per call (all KV heads) */
@@ -326,6 +328,9 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         c->prefill_sched = sch ? atoi(sch) : 1;
         const char *qk = getenv("G3ATTN_PREFILL_QK");
         c->prefill_x8 = !(qk && strcmp(qk, "exact") == 0);
+        const char *ks = getenv("G3ATTN_PREFILL_SPLITS");
+        const int ksv = ks ? atoi(ks) : 0;
+        c->prefill_ksplit = (ksv == 1 || ksv == 2 || ksv == 4) ? ksv : 0;
         const char *nt = getenv("G3ATTN_DECODE_NT");
         c->nt_loads = nt ? atoi(nt) : 2;
         const char *ff = getenv("G3ATTN_FORWARD_FOLD");
@@ -868,7 +873,8 @@ static int prefill_attention(g3attn_ctx *c, int layer, int start_pos, int n, con
     const long long ldk = ((long long)nk + 63) / 64 * 64;
     const size_t v_bytes = align256((size_t)Hkv * ldk * D * sizeof(uint16_t));
     const int pb = 16 * ((c->prefill_qpw == 32 ? 2 : 1)) * ((8 / (c->prefill_qpw == 32 ? 2 : 1)) / c->group);
-    const int S = prefill_splits(n, hist, nk, is_global ? INT_MAX / 2 : W, pb, Hkv, Hq, c->n_cu);
+    const int S = c->prefill_ksplit ? c->prefill_ksplit
+                                    : prefill_splits(n, hist, nk, is_global ? INT_MAX / 2 : W, pb, Hkv, Hq, c->n_cu);
     const size_t po_bytes = S > 1 ? align256((size_t)S * n * Hq * D * sizeof(float)) : 0;
     const size_t pml_bytes = S > 1 ? align256((size_t)S * n * Hq * 2 * sizeof(float)) : 0;
     /* the fp8 cross policy's key-scale bytes, one per staged key row */

@@ -322,6 +322,21 @@ def test_key_splits(built, tmp_path, variant, order):
         assert e.threads["prefill_kernel"] == (256 if variant == "qpw32" else 512)
 
 
+@pytest.mark.parametrize("splits", [1, 4])
+def test_forced_split_counts(built, tmp_path, splits):
+    """G3ATTN_PREFILL_SPLITS: a local prefill whose blocks see the window and
+    the history before them (four or five tiles each, so four splits leave
+    one or two tiles per part), forced to 1 and to 4 key splits, then a
+    decode over the same cache."""
+    e = Emu(tmp_path, H=2, Hkv=1, max_context=640, window=64)
+    e.prefill(0, 0, 100)
+    e.prefill(0, 100, 192)
+    e.decode(0, 292)
+    launches = e.run(G3ATTN_PREFILL_SPLITS=splits)
+    # the 192-token call: 3 blocks x splits workgroups; the first call 2 x splits
+    assert launches["prefill_kernel"] == (2, 5 * splits), launches
+
+
 def test_fp32_values_take_the_v_lo_pass(built, tmp_path):
     """Inputs that are not bf16-valued: the staging kernel flags V_lo and the
     kernel adds the P_hi.V_lo pass; also with QK-norm absent."""

@@ -350,6 +350,27 @@ def test_split_merge_repeats_in_one_context(ctx8k):
                 assert np.array_equal(got, first[i]), (rep, i)
 
 
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_forced_split_counts(monkeypatch, splits):
+    """G3ATTN_PREFILL_SPLITS forces the key-split count: a local prefill with
+    cached history across the ring wrap and a 2048-token global prefill, each
+    run with 1, 2 and 4 splits (4 leaves some of the local blocks' parts with
+    a single tile, and splits past a block's tiles empty), against the oracle;
+    the library reports the count it ran."""
+    monkeypatch.setenv("G3ATTN_PREFILL_SPLITS", str(splits))
+    cases = [PrefillCase(72, layer=3, start_pos=1500, n=700, max_context=4096),
+             PrefillCase(73, layer=5, start_pos=0, n=2048, max_context=4096)]
+    with _ctx(max_context=4096, num_layers=12) as c:
+        for i, case in enumerate(cases):
+            got = case.gpu(c)
+            assert c.last_splits(1) == splits, (i, c.last_splits(1))
+            want, Kc, Vc = case.oracle()
+            err = rel_err(got, want)
+            print(f"[forced splits {splits} case {i}] rel_err={err:.3e}", flush=True)
+            assert err <= TOL, (splits, i, err)
+            _check_cache(c, case, Kc, Vc)
+
+
 def test_exact_score_policy(monkeypatch):
     """G3ATTN_PREFILL_QK=exact (three fp16 score passes, the key rows staged
     fp16 hi | lo) on the forms cases: each within 5e-4 x RMS of the oracle

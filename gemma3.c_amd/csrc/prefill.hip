@@ -9,19 +9,25 @@
 // Precision policy.  Post-RoPE q and k, P and V are fp32 and not
 // representable in any MFMA input format, and the path is held to max-abs
 // error <= 2e-3 x output RMS.  A single bf16 or fp16 pass misses that bar by
-// 5-60x on the early causal rows, so every operand is split, x = x_hi + x_lo:
-//   S = q.k   three fp16 MFMA passes  q_hi.k_hi + q_lo.k_hi + q_hi.k_lo
-//             (x_hi = fp16(x), x_lo = fp16(x - x_hi): about 22 bits);
+// 5-60x on the early causal rows, so every operand is split, x = x_hi + x_lo
+// (x_hi = fp16(x) for q and k, bf16(x) for P and V):
+//   S = q.k   q_hi.k_hi + q_lo.k_hi + q_hi.k_lo, by default one fp16 MFMA pass
+//             for q_hi.k_hi and the two cross terms as one scaled fp8 MFMA dot
+//             with per-key and per-query power-of-two scales (tile_scores);
+//             with the exact policy three fp16 passes (x_lo = fp16(x - x_hi));
 //   O = P.V   bf16 MFMA passes        P_hi.V_hi + P_lo.V_hi (+ P_hi.V_lo)
 //             (16 bits of P and V).  The staging pass records whether any
 //             V_lo is nonzero; when every staged value is exactly bf16 (the
 //             bf16-valued inputs the path is specified on) V_lo is zero and
 //             its pass is skipped, which changes no bit of the result.
-// fp32 accumulation throughout: 2.5x (3x with V_lo) the algorithmic MFMA work.
+// fp32 accumulation throughout: 2.5x (3x with V_lo) the algorithmic MFMA
+// FLOPs; in MFMA-pipe time 2x under the fp8 cross policy (its fp8 MFMAs run
+// at twice the fp16 rate).
 //
 // Data flow.  One workgroup = 8 / NQB waves = one KV head x the queries of
 // its G query heads; each wave owns NQB blocks of 16 queries of one head over
-// the full head dim (per block Q^T hi / lo: 64 VGPRs, O^T: 64):
+// the full head dim (per block Q^T hi / lo or hi / fp8 cross operand: 64
+// VGPRs, O^T: 64):
 //   S^T[key][query] = K . Q^T   with v_mfma_f32_16x16x32_f16: A = K tile rows
 //     from LDS, B = the wave's Q^T fragments in registers;
 //   O^T[dim][query] += V^T . P^T with v_mfma_f32_16x16x32_bf16: A = V^T tile
@@ -36,7 +42,8 @@
 // deep, filled by gfx950's direct buffer -> LDS loads (buffer_load_dwordx4
 // ... lds: no staging registers; one wave instruction moves 1 KiB in lane
 // order; the addresses are a scalar buffer descriptor + one per-lane offset):
-//   K: one 1 KiB LDS row per key, fp16 hi (512 B) | lo (512 B), its 16-byte
+//   K: one 1 KiB LDS row per key, fp16 hi (512 B) | lo (512 B) or | the fp8
+//      cross operand bytes (512 B, G3K_KROW_X8 in g3k.h), its 16-byte
 //      chunks XOR-swizzled by key bits (kswz), so the 16 rows one fragment
 //      read touches hit 16 bank groups; every fragment address is one of
 //      four per-lane bases + an immediate offset;
@@ -529,12 +536,27 @@ __device__ __forceinline__ void attend(const g3k_prefill_args &p, unsigned char 
     // 1-D grid, longest (latest) query blocks first across all heads: with
     // workgroups dealt round-robin to the 8 XCDs, block id -> (qb, id % H_kv)
     // also keeps each XCD on one KV head (its L2 streams one head's K / V).
-    // with key splits, block id -> (qb, split, kvh), kvh fastest
-    const int kvh = blockIdx.x % p.n_kv_heads;
+    // With key splits, block id -> (qb, split, kvh), kvh fastest; when H_kv
+    // divides 8 and the blocks fill whole groups of Q = 8 / H_kv, the splits
+    // of one (qb, kvh) are 8 ids apart instead (ids sg * 8 S + split * 8 +
+    // (qb % Q) * H_kv + kvh), so they share an XCD and its L2 serves the
+    // block's query rows and RoPE rows once for all of them.
     const int S = p.ksplit;
-    const int pair = (int)(blockIdx.x / p.n_kv_heads);
-    const int split = pair % S;
-    const int qb = (int)(gridDim.x / (p.n_kv_heads * S)) - 1 - pair / S;
+    const int nbq = (int)(gridDim.x / (p.n_kv_heads * S));   // query blocks
+    int kvh, split, qbi;
+    if (S > 1 && 8 % p.n_kv_heads == 0 && nbq % (8 / p.n_kv_heads) == 0) {
+        const int Q = 8 / p.n_kv_heads;
+        const int id = (int)blockIdx.x, sg = id / (8 * S), r = id % (8 * S);
+        split = r / 8;
+        kvh = (r % 8) % p.n_kv_heads;
+        qbi = sg * Q + (r % 8) / p.n_kv_heads;
+    } else {
+        kvh = blockIdx.x % p.n_kv_heads;
+        const int pair = (int)(blockIdx.x / p.n_kv_heads);
+        split = pair % S;
+        qbi = pair / S;
+    }
+    const int qb = nbq - 1 - qbi;
     const int qhead = kvh * G + wave / WPH;
     // uniform, so the wave's query range and tile bounds below stay in
     // SGPRs (the head and the phase order stay per lane: as uniform values

@@ -411,6 +411,11 @@ __device__ __forceinline__ void tile_scores(f32x4 (&s)[NQB][2], const unsigned c
 template <bool X8>
 __device__ __forceinline__ void load_queries(half8 (&qh)[8], u32x4 (&qlo)[8], int &sb, const g3k_prefill_args &p,
                                              int tok, int qhead, int n_heads, int g) {
+    // Arithmetic exactly as written (explicit fmaf where fused): how the
+    // compiler would otherwise fuse multiplies into adds can differ between
+    // the kernel forms this is inlined into, and the forms must agree bit for
+    // bit.
+#pragma clang fp contract(off)
     const bool qv = tok < p.n;
     const float *qrow = p.q + ((size_t)(qv ? tok : 0) * n_heads + qhead) * D + 8 * g;
     const float *rrow = p.rope + (size_t)(p.start_pos + (qv ? tok : 0)) * D + 2 * 8 * g;
@@ -443,15 +448,17 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], u32x4 (&qlo)[8], in
 #pragma unroll
         for (int t = 0; t < 8; t++)
 #pragma unroll
-            for (int u = 0; u < 8; u++) ss += x[t][u] * x[t][u];
+            for (int u = 0; u < 8; u++) ss = fmaf(x[t][u], x[t][u], ss);
         ss = col4_sum(ss);
-        const float r = 1.0f / sqrtf(ss / (float)D + p.eps);
+        // x r (1 + w) with the softmax scale folded into r (RoPE is linear),
+        // and zero for a query column past the batch
+        const float rq = qv ? (1.0f / sqrtf(ss / (float)D + p.eps)) * p.qscale : 0.f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const uint32_t w[4] = {wv[t].x, wv[t].y, wv[t].z, wv[t].w};
 #pragma unroll
             for (int u = 0; u < 8; u++)
-                x[t][u] = x[t][u] * r * (1.0f + bf16f((w[u >> 1] >> (16 * (u & 1))) & 0xffff));
+                x[t][u] = x[t][u] * fmaf(rq, bf16f((w[u >> 1] >> (16 * (u & 1))) & 0xffff), rq);
         }
     }
 #pragma unroll
@@ -463,17 +470,19 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], u32x4 (&qlo)[8], in
             for (int e = 0; e < 2; e++) {
                 const int u = 2 * h + e;
                 const float a = x[t][u], b = x[t + 4][u];
-                x[t][u] = a * c[e] - b * sn[e];
-                x[t + 4][u] = a * sn[e] + b * c[e];
+                x[t][u] = fmaf(a, c[e], -(b * sn[e]));
+                x[t + 4][u] = fmaf(a, sn[e], b * c[e]);
             }
         }
     }
+    // without QK-norm the scale (and the zero past the batch) comes here
+    const float qsc = p.q_norm ? 1.f : (qv ? p.qscale : 0.f);
     float mloc = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++)
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const float v = qv ? x[t][u] * p.qscale : 0.f;
+            const float v = x[t][u] * qsc;
             const _Float16 hi = (_Float16)v;
             qh[t][u] = hi;
             x[t][u] = v - (float)hi;      // the low part, exact in fp32

@@ -58,7 +58,7 @@ template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 #define G3K_DECODE_LDSMERGE 1   // lane-groups' partials summed in the LDS merge, not by cross-lane swaps
 #endif
 #ifndef G3K_DECODE_DB
-#define G3K_DECODE_DB 1   // double-buffered row steps (see the row loop); 0: single set
+#define G3K_DECODE_DB 1   // double-buffered row steps at group <= 2 (see the row loop); 0: single set
 #endif
 constexpr float NEG_BIG = -1.0e30f;  // "no row seen yet": finite so exp2 never sees inf - inf
 // Measured on MI355X: two workgroups per CU (<= 256 VGPRs), one 8-row step
@@ -338,7 +338,10 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     }
 
     // ---- stream this split's rows ----
-#if G3K_DECODE_DB
+    // Double-buffered row steps where the registers allow them (group <= 2;
+    // at group 4 the second set spilled to scratch)
+    constexpr bool DB = G3K_DECODE_DB && G <= 2;
+    if constexpr (DB) {
     // Two register sets: the next step's loads are issued before the current
     // step is reduced, so each wave keeps a step in flight while it computes.
     // The last step is peeled, so every load in the loop body is
@@ -367,14 +370,14 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
             base = nb;
         }
     }
-#else
+    } else {
     // reduce the loaded step, then load the next
     while (base < c1) {
         step_compute<G, R, FUSED>(kk, vv, qv, m, l, acc, base, c1, grp, p.mask);
         base += stride;
         if (base < c1) load_step<R, NTL>(kk, vv, kbase, vbase, p.row_stride, p.head_stride, base, c1, p.skip, grp, c);
     }
-#endif
+    }
 
 #if G3K_DECODE_LDSMERGE
     // ---- every lane-group's (l, acc) to LDS as it is (the four groups of a

@@ -482,7 +482,7 @@ __device__ __forceinline__ void load_queries(half8 (&qh)[8], u32x4 (&qlo)[8], in
     for (int t = 0; t < 8; t++)
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const float v = x[t][u] * qsc;
+            const float v = p.q_norm ? x[t][u] : x[t][u] * qsc;
             const _Float16 hi = (_Float16)v;
             qh[t][u] = hi;
             x[t][u] = v - (float)hi;      // the low part, exact in fp32

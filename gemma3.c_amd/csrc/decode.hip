@@ -54,9 +54,6 @@ template <int G> constexpr int rows_for() { return G3K_DECODE_ROWS; }
 #else
 template <int G> constexpr int rows_for() { return G >= 4 ? 1 : 2; }
 #endif
-#ifndef G3K_DECODE_LDSMERGE
-#define G3K_DECODE_LDSMERGE 1   // lane-groups' partials summed in the LDS merge, not by cross-lane swaps
-#endif
 #ifndef G3K_DECODE_DB
 #define G3K_DECODE_DB 1   // double-buffered row steps at group <= 2 (see the row loop); 0: single set
 #endif
@@ -256,10 +253,9 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = lane >> 4, c = lane & 15;
 
-    // per wave (G3K_DECODE_LDSMERGE 0) or per lane-group (1) partials
-    constexpr int NP = G3K_DECODE_LDSMERGE ? 4 * NW : NW;
-    __shared__ float s_acc[NP][G * D];
-    __shared__ float s_m[NW][G], s_l[NP][G];
+    // the partials of every lane-group (four per wave) for the merge
+    __shared__ float s_acc[4 * NW][G * D];
+    __shared__ float s_m[NW][G], s_l[4 * NW][G];
 
     const float *kbase = p.kc + (size_t)kvh * p.head_stride;
     const float *vbase = p.vc + (size_t)kvh * p.head_stride;
@@ -379,9 +375,9 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     }
     }
 
-#if G3K_DECODE_LDSMERGE
     // ---- every lane-group's (l, acc) to LDS as it is (the four groups of a
-    // wave share m, so the merge below only adds them): no cross-lane sums ----
+    // wave share m, so the merge below only adds them; adding them across lanes
+    // first, with permlane swaps, was 0.9-1 us slower per 8K decode step) ----
 #pragma unroll
     for (int g = 0; g < G; g++) store16(&s_acc[4 * wave + grp][g * D], acc[g], c);
     if (c == 0) {
@@ -392,32 +388,6 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
 #pragma unroll
         for (int g = 0; g < G; g++) s_m[wave][g] = m[g];
     }
-#else
-    // ---- merge the four lane-groups of each wave (they share m) ----
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        l[g] = col4_sum(l[g]);
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float a = acc[g][j][e];
-                a = col4_sum(a);
-                acc[g][j][e] = a;
-            }
-    }
-    if (grp == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++) store16(&s_acc[wave][g * D], acc[g], c);
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            s_m[wave][g] = m[g];
-            s_l[wave][g] = l[g];
-        }
-    }
-#endif
     __syncthreads();
 
     // ---- merge the waves: this workgroup's (m, l, acc) per query head, stored
@@ -435,15 +405,10 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             const float f = fast_exp2(s_m[w][g] - M);
-#if G3K_DECODE_LDSMERGE
             const float lw = (s_l[4 * w][g] + s_l[4 * w + 1][g]) + (s_l[4 * w + 2][g] + s_l[4 * w + 3][g]);
             const float aw = (s_acc[4 * w][e] + s_acc[4 * w + 1][e]) + (s_acc[4 * w + 2][e] + s_acc[4 * w + 3][e]);
             L += lw * f;
             A += aw * f;
-#else
-            L += s_l[w][g] * f;
-            A += s_acc[w][e] * f;
-#endif
         }
         if (p.n_splits == 1) {   // uniform
             out[e] = A / L;

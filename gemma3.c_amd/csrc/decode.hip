@@ -22,9 +22,18 @@
 //   Softmax runs in the exp2 domain: q is pre-scaled by scale*log2(e).
 //   Waves merge through LDS; with more than one split each workgroup writes
 //   an (m, l, acc) partial and a second small launch (combine_kernel)
-//   merges them.  A last-arrival merge inside the kernel (an arrival counter
-//   per KV head, one agent-scope release per workgroup, the last workgroup
-//   merging) was measured no faster for local layers and slower at 8K.
+//   merges them.
+//
+// One-launch form (XM, local layers: <= 32 splits): the grid is ordered so
+// that all splits of one run of query heads have workgroup ids equal mod 8,
+// which the MI355X dispatcher places on one XCD (the host checks this with
+// a probe launch per context).  Each split's partial then lands in that
+// XCD's L2, the last workgroup to count itself in the run's L2 counter
+// merges the run's partials from there, and no combine launch follows.  With
+// 4 KV heads the 8 runs are the 8 query heads (one head per workgroup), so
+// every XCD takes part and each KV head's window is read twice.  A merge at
+// the device's point of coherence instead (agent-scope stores, counter and
+// loads, any placement) was measured slower than the second launch.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <pthread.h>
@@ -246,11 +255,76 @@ __device__ __forceinline__ void swap_merge(float &M, float &L, float4 &A) {
     merge_ml(M, L, A, m.y, l.y, make_float4(ax.y, ay.y, az.y, aw.y));
 }
 
-template <int G, bool FUSED, bool NTL>
+// The one-launch form's merge of a run's n_splits (<= G3K_XM_MAX_SPLITS)
+// partials, in split order: out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M)
+// l_s.  Thread t owns dim t of each of the G heads (NT == D); all of a
+// head's partial loads are issued at once (one L2 round trip).  Splits past
+// n_splits read the last split's partial and weigh it 0.
+template <int G>
+__device__ __forceinline__ void xm_merge(const g3k_decode_args &p, int kvh, int gq0, int GF, int tid) {
+    static_assert(NT == D, "one thread per dim");
+    const int S = p.n_splits;
+    constexpr int CP_SC0 = 1;   // cache policy: bypass the L1
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int h = gq0 + g;
+        // run h's partial of split s: ws_acc[((kvh * MAX + s) * GF + h) * D + d]
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+            p.ws_acc + ((size_t)kvh * G3K_MAX_SPLITS * GF + h) * D, (short)0, S * GF * D * 4, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+            p.ws_ml + ((size_t)kvh * G3K_MAX_SPLITS * GF + h) * 2, (short)0, S * GF * 2 * 4, 0x00020000);
+        uint32_t a[G3K_XM_MAX_SPLITS], ml[G3K_XM_MAX_SPLITS][2];
+#pragma unroll
+        for (int s = 0; s < G3K_XM_MAX_SPLITS; s++) {
+            const int sc = s < S ? s : S - 1;
+            a[s] = __builtin_amdgcn_raw_buffer_load_b32(ra, (unsigned)((sc * GF * D + tid) * 4), 0, CP_SC0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rm, (unsigned)(sc * GF * 2 * 4), 0, CP_SC0);
+            ml[s][0] = v[0];
+            ml[s][1] = v[1];
+        }
+        // every load above is issued before the first use below
+        __builtin_amdgcn_sched_barrier(0);
+        float ms[G3K_XM_MAX_SPLITS];
+#pragma unroll
+        for (int s = 0; s < G3K_XM_MAX_SPLITS; s++) ms[s] = s < S ? __uint_as_float(ml[s][0]) : NEG_BIG;
+        float M = ms[0];
+#pragma unroll
+        for (int s = 1; s < G3K_XM_MAX_SPLITS; s++) M = fmaxf(M, ms[s]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int s = 0; s < G3K_XM_MAX_SPLITS; s++) {
+            const float f = fast_exp2(ms[s] - M);
+            L += __uint_as_float(ml[s][1]) * f;
+            A += __uint_as_float(a[s]) * f;
+        }
+        p.out[(size_t)(kvh * GF + h) * D + tid] = A / L;
+    }
+}
+
+template <int G, bool FUSED, bool NTL, bool XM>
 __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     constexpr int R = rows_for<G>();
     constexpr int ROWS_PER_WAVE_STEP = 4 * R;
-    const int split = blockIdx.x, kvh = blockIdx.y;
+    // Two-launch form: grid (n_splits, H_kv), the workgroup serves all G query
+    // heads of its KV head.  One-launch form (XM): a 1-D grid of PP * n_splits
+    // workgroups for P = H_kv * GF / G runs of G query heads (the group GF
+    // split into runs), PP = P rounded up to a multiple of 8; run pg of split
+    // s is workgroup s * PP + pg, so every split of a run has the same id
+    // mod 8.  Workgroups pg >= P have no run and end at once.
+    const int GF = XM ? p.group : G;
+    int split, kvh, gq0, pg = 0;
+    if constexpr (XM) {
+        const int runs = GF / G, P = p.n_kv_heads * runs, PP = (P + 7) & ~7;
+        pg = (int)blockIdx.x % PP;
+        if (pg >= P) return;
+        split = (int)blockIdx.x / PP;
+        kvh = pg / runs;
+        gq0 = (pg % runs) * G;
+    } else {
+        split = blockIdx.x;
+        kvh = blockIdx.y;
+        gq0 = 0;
+    }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, grp = lane >> 4, c = lane & 15;
 
     // the partials of every lane-group (four per wave) for the merge
@@ -289,7 +363,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     }
 #pragma unroll
     for (int g = 0; g < G; g++) {
-        load16(qv[g], p.q + (size_t)(kvh * G + g) * D, c);
+        load16(qv[g], p.q + (size_t)(kvh * GF + gq0 + g) * D, c);
         if (FUSED) norm_rope16(qv[g], p.k_norm ? p.q_norm : nullptr, p.eps, cs, sn, c);
 #pragma unroll
         for (int j = 0; j < 4; j++)
@@ -311,7 +385,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     // ---- the new token (fused decode): split 0, wave 0 seeds its state with it ----
     if (seeds) {
         norm_rope16(kn, p.q_norm ? p.k_norm : nullptr, p.eps, cs, sn, c);
-        if (grp == 0) {
+        if (grp == 0 && gq0 == 0) {   // one writer per KV head
             store16(p.kc + (size_t)kvh * p.head_stride + (size_t)p.new_slot * p.row_stride, kn, c);
             store16(p.vc + (size_t)kvh * p.head_stride + (size_t)p.new_slot * p.row_stride, vn, c);
         }
@@ -394,7 +468,7 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
     // straight from the merging thread (every thread of a head computes the
     // same M and L): the normalised output with one split, else this split's
     // partial ----
-    float *out = p.out + (size_t)kvh * G * D;
+    float *out = p.out + (size_t)(kvh * GF + gq0) * D;
     const size_t slot = (size_t)kvh * G3K_MAX_SPLITS + split;
     for (int e = tid; e < G * D; e += NT) {
         const int g = e / D;
@@ -413,12 +487,36 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
         if (p.n_splits == 1) {   // uniform
             out[e] = A / L;
         } else {
-            p.ws_acc[slot * G * D + e] = A;
+            p.ws_acc[(slot * GF + gq0) * D + e] = A;
             if (e % D == 0) {
-                p.ws_ml[(slot * G + g) * 2] = M;
-                p.ws_ml[(slot * G + g) * 2 + 1] = L;
+                p.ws_ml[(slot * GF + gq0 + g) * 2] = M;
+                p.ws_ml[(slot * GF + gq0 + g) * 2 + 1] = L;
             }
         }
+    }
+    if constexpr (XM) {
+        if (p.n_splits == 1) return;
+        // Last-arrival merge on this XCD.  Every split of this run stores its
+        // partial with plain stores, which land in the XCD's L2 (the vector L1
+        // writes through); the wait below (vmcnt counts stores on this family)
+        // and the barrier put all of this workgroup's stores there before it
+        // counts itself.  The counter is a workgroup-scope atomic, performed
+        // in that same L2: the runs never span XCDs (the host checks the
+        // workgroup -> XCD placement first), so the L2 orders the arrivals and
+        // holds every partial, with no write-back to memory and no cache
+        // invalidation.  The last to arrive resets the counter for the next
+        // launch and reads the partials past its L1 (sc0 loads).
+        G3K_WAIT_VMEM();
+        __syncthreads();
+        __shared__ int s_last;
+        if (tid == 0) {
+            unsigned *cnt = p.xm_count + (size_t)pg * G3K_XM_COUNTER_STRIDE;
+            const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            s_last = old == (unsigned)(p.n_splits - 1);
+            if (s_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __syncthreads();
+        if (s_last) xm_merge<G>(p, kvh, gq0, GF, tid);
     }
 }
 
@@ -508,11 +606,21 @@ template <int G, bool FUSED, bool NTL>
 hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
     dim3 grid(a->n_splits, a->n_kv_heads);
     // With timing events the dispatch itself records them (kernel begin / end).
-    hipExtLaunchKernelGGL((decode_kernel<G, FUSED, NTL>), grid, dim3(NT), 0, st, (hipEvent_t)a->ev0,
+    hipExtLaunchKernelGGL((decode_kernel<G, FUSED, NTL, false>), grid, dim3(NT), 0, st, (hipEvent_t)a->ev0,
                           (hipEvent_t)a->ev1, 0, *a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a->n_splits == 1) return e;
     hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 32, G, a->n_kv_heads), dim3(NT), 0, st, *a);
+    return hipGetLastError();
+}
+
+// One-launch form: runs of GW query heads (GW divides the group), P = H_kv *
+// group / GW runs, padded to PP, a multiple of 8.
+template <int GW, bool NTL>
+hipError_t launch_xm(const g3k_decode_args *a, hipStream_t st) {
+    const int PP = (a->n_kv_heads * (a->group / GW) + 7) & ~7;
+    hipExtLaunchKernelGGL((decode_kernel<GW, true, NTL, true>), dim3(PP * a->n_splits), dim3(NT), 0, st,
+                          (hipEvent_t)a->ev0, (hipEvent_t)a->ev1, 0, *a);
     return hipGetLastError();
 }
 
@@ -522,11 +630,16 @@ hipError_t launch_g(const g3k_decode_args *a, int fused, hipStream_t st) {
     return a->nt_loads ? launch<G, true, true>(a, st) : launch<G, true, false>(a, st);
 }
 
+__global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned *xcc, int n) {
+    unsigned v = G3K_XCC_ID();
+    if (threadIdx.x == 0 && (int)blockIdx.x < n) xcc[blockIdx.x] = v & 0xf;
+}
+
 template <int G, bool FUSED>
 int capacity() {
     int per_cu = 0, cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<G, FUSED, FUSED>, NT, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<G, FUSED, FUSED, false>, NT, 0) != hipSuccess)
         return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     return per_cu * cus;
@@ -538,6 +651,16 @@ extern "C" int g3k_decode(const g3k_decode_args *a, int fused, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (a->n_splits < 1 || a->n_splits > G3K_MAX_SPLITS || a->rows_per_split % G3K_SPLIT_GRAIN)
         return (int)hipErrorInvalidValue;
+    if (a->xm_heads) {
+        // the one-launch form: fused decode, 2..G3K_XM_MAX_SPLITS splits, runs
+        // of 1 or 2 query heads dividing the group
+        const int gw = a->xm_heads;
+        if (!fused || !a->xm_count || a->n_splits < 2 || a->n_splits > G3K_XM_MAX_SPLITS ||
+            (gw != 1 && gw != 2) || a->group % gw)
+            return (int)hipErrorInvalidValue;
+        if (gw == 1) return (int)(a->nt_loads ? launch_xm<1, true>(a, st) : launch_xm<1, false>(a, st));
+        return (int)(a->nt_loads ? launch_xm<2, true>(a, st) : launch_xm<2, false>(a, st));
+    }
     switch (a->group) {
         case 1: return (int)launch_g<1>(a, fused, st);
         case 2: return (int)launch_g<2>(a, fused, st);
@@ -697,6 +820,12 @@ extern "C" int g3k_gqa_generic(const g3k_gqa_args *a, void *stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a->n_splits == 1) return (int)e;
     hipLaunchKernelGGL(gqa_generic_combine_kernel, dim3(a->n_heads), dim3(NT), 0, st, *a);
+    return (int)hipGetLastError();
+}
+
+extern "C" int g3k_xcd_probe(unsigned *xcc, int n, void *stream) {
+    if (n < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(xcd_probe_kernel, dim3(n), dim3(64), 0, (hipStream_t)stream, xcc, n);
     return (int)hipGetLastError();
 }
 

@@ -51,7 +51,24 @@ typedef struct {
     float *ws_ml;          /* [H_kv][G3K_MAX_SPLITS][group][2] (max, sum) */
     int nt_loads;          /* fused decode: K/V rows through non-temporal buffer loads */
     void *ev0, *ev1;       /* hipEvent_t: begin / end of decode_kernel's dispatch, or NULL */
+    /* One-launch form (xm_heads > 0): workgroups of xm_heads query heads,
+     * the splits of each (KV head, query-head run) on one XCD, merged there
+     * by the last to arrive (G3K_XM_* below); 0: decode + combine launches. */
+    int xm_heads;
+    unsigned *xm_count;    /* G3K_XM_COUNTERS(H_q) zeroed arrival counters */
 } g3k_decode_args;
+
+/* One-launch decode: at most this many splits, and the arrival counters,
+ * one per (KV head, query-head run) and G3K_XM_COUNTER_STRIDE apart (their
+ * own 256-byte line each), in a zeroed buffer that every launch leaves zero. */
+#define G3K_XM_MAX_SPLITS 32
+#define G3K_XM_COUNTER_STRIDE 64
+#define G3K_XM_COUNTERS(n_heads) ((size_t)(n_heads) * G3K_XM_COUNTER_STRIDE)
+
+/* Writes the XCD (hardware register XCC_ID) each workgroup of an n-workgroup
+ * launch ran on to xcc[n].  The one-launch decode needs workgroups whose ids
+ * agree mod 8 to run on one XCD.  Returns a hipError_t. */
+int g3k_xcd_probe(unsigned *xcc, int n, void *stream);
 
 /* QK-norm + RoPE of q (and of the new k), cache write of the new k/v and
  * split-K attention over the cache; with n_splits > 1 a second launch

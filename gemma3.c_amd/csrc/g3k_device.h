@@ -14,6 +14,20 @@
 #define G3K_WAIT_VMEM() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
 #endif
 
+// The XCD this wave runs on: the hardware register XCC_ID (gfx940 and
+// later), whose low 4 bits number the XCDs.  The host-emulation build
+// defines it as the workgroup id mod 8.
+#ifndef G3K_XCC_ID
+#define G3K_XCC_ID() g3k::xcc_id()
+namespace g3k {
+__device__ __forceinline__ unsigned xcc_id() {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v;
+}
+}  // namespace g3k
+#endif
+
 namespace g3k {
 
 template <int CTRL>

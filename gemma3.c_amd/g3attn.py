@@ -323,7 +323,9 @@ class Context:
         return ms.value, n.value
 
     def last_splits(self, kind: int) -> int:
-        """Key splits the last call of kind 0 (decode) or 1 (prefill) chose."""
+        """Key splits the last call of kind 0 (decode) or 1 (prefill) chose;
+        kind 2: query heads per workgroup of the last decode's one-launch
+        form (0: decode + combine launches, or one split)."""
         n = C.c_int()
         _check(lib().g3attn_last_splits(self._h, kind, C.byref(n)))
         return n.value

@@ -135,6 +135,12 @@ struct g3attn_ctx {
     /* prefill key splits: per (query block, KV head) arrival counters, zeroed
      * once; each call's S arrivals wrap them back to zero */
     unsigned *d_arrive;
+    /* one-launch decode: arrival counters (G3K_XM_COUNTERS), zeroed once and
+     * left zero by every launch; xm_ok: the workgroup -> XCD placement probe
+     * passed at create; xmerge: G3ATTN_DECODE_XMERGE (0 off, 1 local layers,
+     * 2 every layer with few enough splits) */
+    unsigned *d_xcount;
+    int xm_ok, xmerge;
     /* kernel timing (g3attn_profile_*): event pairs per kind */
     struct {
         int on;
@@ -143,7 +149,7 @@ struct g3attn_ctx {
         double ms[2];
         int count[2];
     } prof;
-    int last_splits[2]; /* g3attn_last_splits: decode, prefill */
+    int last_splits[3]; /* g3attn_last_splits: decode, prefill, decode heads per one-launch workgroup */
     int split_rows; /* 0 = heuristic */
     int min_rows;   /* smallest heuristic split */
     int prefill_qpw; /* prefill queries per wave: 16 or 32 (G3ATTN_PREFILL_QPW) */
@@ -195,6 +201,7 @@ static void ctx_free(g3attn_ctx *c) {
     hipFree(c->d_pf);
     hipFree(c->d_vflag);
     hipFree(c->d_arrive);
+    hipFree(c->d_xcount);
     hipFree(c->d_la);
     hipFree(c->d_fw);
     hipFree(c->d_wt);
@@ -238,6 +245,30 @@ static int alloc_dev(void **p, size_t bytes, const char *what) {
 /* Decode combine workspace: split slots [H_kv][G3K_MAX_SPLITS], each
  * group * head_dim floats (+ group * 2 for max and sum). */
 static size_t ws_slots(int n_kv) { return (size_t)n_kv * G3K_MAX_SPLITS; }
+
+/* The one-launch decode merges each run's splits in one XCD's L2, so it
+ * needs the workgroups whose ids agree mod 8 to run on one XCD (the MI355X
+ * dispatcher deals workgroup i to XCD i mod 8).  Checked once per context
+ * on a 512-workgroup probe launch; any mismatch, or a failed launch, keeps
+ * every decode on the two-launch form. */
+static int xcd_placement_ok(g3attn_ctx *c) {
+    enum { N = 512 };
+    unsigned *d = NULL, h[N];
+    int ok = 0;
+    if (hipMalloc((void **)&d, sizeof h) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    if (g3k_xcd_probe(d, N, c->stream) == hipSuccess &&
+        hipMemcpyAsync(h, d, sizeof h, hipMemcpyDeviceToHost, c->stream) == hipSuccess &&
+        hipStreamSynchronize(c->stream) == hipSuccess) {
+        ok = 1;
+        for (int i = 8; i < N; i++) ok &= h[i] == h[i % 8];
+    }
+    (void)hipGetLastError();
+    hipFree(d);
+    return ok;
+}
 
 g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
                           const float *rope_local, const float *rope_global) {
@@ -316,6 +347,12 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         if (hipMemset(c->d_arrive, 0, nb) != hipSuccess) goto fail_rt;
     }
     {
+        const size_t nb = G3K_XM_COUNTERS(cfg->num_heads) * sizeof(unsigned);
+        if (!alloc_dev((void **)&c->d_xcount, nb, "decode arrival counters")) goto fail;
+        if (hipMemset(c->d_xcount, 0, nb) != hipSuccess) goto fail_rt;
+        c->xm_ok = xcd_placement_ok(c);
+    }
+    {
         const char *w = getenv("G3ATTN_DECODE_WGS");
         const char *mr = getenv("G3ATTN_SPLIT_MIN_ROWS");
         int cus = 0;
@@ -331,6 +368,8 @@ g3attn_ctx *g3attn_create(const g3attn_config *cfg, int max_context,
         const char *ks = getenv("G3ATTN_PREFILL_SPLITS");
         const int ksv = ks ? atoi(ks) : 0;
         c->prefill_ksplit = (ksv == 1 || ksv == 2 || ksv == 4) ? ksv : 0;
+        const char *xm = getenv("G3ATTN_DECODE_XMERGE");
+        c->xmerge = xm ? atoi(xm) : 1;
         const char *nt = getenv("G3ATTN_DECODE_NT");
         c->nt_loads = nt ? atoi(nt) : 2;
         const char *ff = getenv("G3ATTN_FORWARD_FOLD");
@@ -468,7 +507,7 @@ int g3attn_profile_read(g3attn_ctx *c, int kind, double *total_ms, int *count) {
 }
 
 int g3attn_last_splits(g3attn_ctx *c, int kind, int *splits) {
-    if (!c || kind < 0 || kind > 1 || !splits) {
+    if (!c || kind < 0 || kind > 2 || !splits) {
         set_err("g3attn_last_splits: bad arguments");
         return G3_ERR_INVALID_ARG;
     }
@@ -556,6 +595,26 @@ int g3attn_upload_rope(g3attn_ctx *c, const float *rope_local, const float *rope
     return G3_OK;
 }
 
+/* Query heads per workgroup of the one-launch decode, or 0 for the
+ * two-launch form.  One launch serves 2..G3K_XM_MAX_SPLITS splits (local
+ * layers: at most 32 splits of 32 rows) when the placement probe passed.
+ * Its runs of query heads fill all 8 XCDs: the whole group per workgroup
+ * where H_kv is a multiple of 8, else one query head per workgroup (H_q a
+ * multiple of 8; each KV head's rows are then read once per query head, by
+ * workgroups on different XCDs).  On MI355X at 8 query / 4 KV heads the one
+ * query head per workgroup took configs[0] from 8.6 to 7.2-7.4 us per call;
+ * whole groups on 4 XCDs (the other 4 idle) took 9.9 us.  Global layers
+ * (G3ATTN_DECODE_XMERGE=2 admits them) would read their long caches twice. */
+static int xm_heads(const g3attn_ctx *c, int n_splits, int is_global) {
+    if (!c->xm_ok || !c->xmerge || (is_global && c->xmerge != 2) || n_splits < 2 ||
+        n_splits > G3K_XM_MAX_SPLITS)
+        return 0;
+    const int n_kv = c->cfg.num_kv_heads, g = c->group;
+    if (g <= 2 && n_kv % 8 == 0) return g;
+    if ((n_kv * g) % 8 == 0) return 1;
+    return 0;
+}
+
 /* One decode step; in_forward: called by the token forward (cache policy
  * below). */
 static int decode_enqueue(g3attn_ctx *c, int layer, int pos, const float *q, const float *k,
@@ -601,6 +660,9 @@ static int decode_enqueue(g3attn_ctx *c, int layer, int pos, const float *q, con
     a.out = attn_out;
     a.ws_acc = c->ws_acc;
     a.ws_ml = c->ws_ml;
+    a.xm_heads = xm_heads(c, a.n_splits, is_global);
+    a.xm_count = c->d_xcount;
+    c->last_splits[2] = a.xm_heads;
     /* Cache policy of the K/V loads (G3ATTN_DECODE_NT = 2).  A global layer
      * streams its whole cache once per token: non-temporal loads keep it
      * from evicting everything else.  Called for attention alone, a local

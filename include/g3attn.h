@@ -349,11 +349,14 @@ int g3attn_profile_enable(g3attn_ctx *ctx, int enable);
 int g3attn_profile_read(g3attn_ctx *ctx, int kind, double *total_ms, int *count);
 
 /* The work split the last call of one kind chose (no counterpart in the
- * reference): kind 0, the decode's key splits per KV head (1 = no combine
- * launch); kind 1, the prefill's key splits per query block (1, 2 or 4;
- * above 1 the last split to arrive merges the parts inside the kernel).
- * 0 before the first call of that kind.  For tests and benchmarks that must
- * know which code path a call took. */
+ * reference): kind 0, the decode's key splits per KV head (1 = no combine);
+ * kind 1, the prefill's key splits per query block (1, 2 or 4; above 1 the
+ * last split to arrive merges the parts inside the kernel); kind 2, the
+ * decode's query heads per workgroup when its splits were merged inside the
+ * kernel by the last to arrive on each XCD, or 0 when a second launch
+ * combined them (or there was one split).  0 before the first call of that
+ * kind.  For tests and benchmarks that must know which code path a call
+ * took. */
 int g3attn_last_splits(g3attn_ctx *ctx, int kind, int *splits);
 
 /* Thread-local message of the last failure on this thread ("" if none). */

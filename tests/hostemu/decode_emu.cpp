@@ -6,7 +6,9 @@
 //
 // <dir>/args.txt: fused group n_kv n_heads cache_floats row_stride
 //                 head_stride n_stream skip new_slot rows_per_split n_splits
-//                 nt_loads has_norm has_mask eps qscale
+//                 nt_loads has_norm has_mask eps qscale [xm_heads]
+// (xm_heads > 0: the one-launch form with that many query heads per
+// workgroup; the run checks that it leaves its arrival counters zero)
 // <dir>/*.bin inputs (raw little-endian): q [H_q*D], k_new / v_new [H_kv*D]
 // (fused), q_norm / k_norm bf16 [D] (has_norm), rope_row [D] (fused),
 // kc / vc [cache_floats] (row r of head h at h*head_stride + r*row_stride),
@@ -56,6 +58,7 @@ int main(int argc, char **argv) {
     int fused, group, n_kv, n_heads, n_stream, skip, new_slot, rps, n_splits, nt_loads, has_norm, has_mask;
     long long cache, row_stride, head_stride;
     float eps, qscale;
+    int xm_heads = 0;
     FILE *f = std::fopen((dir + "/args.txt").c_str(), "r");
     if (!f || std::fscanf(f, "%d %d %d %d %lld %lld %lld %d %d %d %d %d %d %d %d %f %f", &fused, &group, &n_kv,
                           &n_heads, &cache, &row_stride, &head_stride, &n_stream, &skip, &new_slot, &rps,
@@ -63,6 +66,7 @@ int main(int argc, char **argv) {
         std::fprintf(stderr, "decode_emu: bad args.txt\n");
         return 2;
     }
+    if (std::fscanf(f, "%d", &xm_heads) != 1) xm_heads = 0;
     std::fclose(f);
     const size_t D = G3K_HEAD_DIM, qs = (size_t)n_heads * D, ks = (size_t)n_kv * D;
 
@@ -84,6 +88,7 @@ int main(int argc, char **argv) {
     std::vector<float> out(qs, -12345.0f);
     std::vector<float> ws_acc((size_t)n_kv * G3K_MAX_SPLITS * group * D, -1.0f);
     std::vector<float> ws_ml((size_t)n_kv * G3K_MAX_SPLITS * group * 2, -1.0f);
+    std::vector<unsigned> xcount(G3K_XM_COUNTERS(n_heads), 0u);
 
     g3k_decode_args a = {};
     a.q = q.data();
@@ -110,11 +115,18 @@ int main(int argc, char **argv) {
     a.ws_acc = ws_acc.data();
     a.ws_ml = ws_ml.data();
     a.nt_loads = nt_loads;
+    a.xm_heads = xm_heads;
+    a.xm_count = xm_heads ? xcount.data() : nullptr;
     const int rc = g3k_decode(&a, fused, nullptr);
     if (rc) {
         std::fprintf(stderr, "decode_emu: g3k_decode returned %d\n", rc);
         return 1;
     }
+    for (unsigned v : xcount)
+        if (v) {
+            std::fprintf(stderr, "decode_emu: an arrival counter was left at %u\n", v);
+            return 1;
+        }
     write_bin(dir + "/out.bin", out);
     write_bin(dir + "/kc_out.bin", kc);
     write_bin(dir + "/vc_out.bin", vc);

@@ -89,6 +89,9 @@ hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int *n, K, int, size_t) 
 // Loads complete when issued here, so the library's explicit wait for them
 // is empty.
 #define G3K_WAIT_VMEM() ((void)0)
+// The emulated machine deals workgroup i to XCD i mod 8, as the MI355X
+// dispatcher does.
+#define G3K_XCC_ID() (blockIdx.x % 8u)
 
 // ---- the emulated machine ------------------------------------------------------
 // One fiber per thread of the workgroup, all on the calling OS thread: a
@@ -217,6 +220,9 @@ inline void __threadfence() {}
 #ifndef __HIP_MEMORY_SCOPE_AGENT
 #define __HIP_MEMORY_SCOPE_AGENT 4
 #endif
+#ifndef __HIP_MEMORY_SCOPE_WORKGROUP
+#define __HIP_MEMORY_SCOPE_WORKGROUP 3
+#endif
 inline unsigned atomicInc(unsigned *p, unsigned v) {
     const unsigned old = *p;
     *p = old >= v ? 0u : old + 1u;
@@ -319,8 +325,28 @@ inline void hostemu_raw_buffer_store_b128(T v, __amdgpu_buffer_rsrc_t r, unsigne
     if (off + 16 > r.num_records) hostemu::fail("buffer store beyond num_records");
     std::memcpy(const_cast<char *>(r.base) + off, &v, 16);
 }
+// 4- and 8-byte buffer loads into registers, range-checked like the b128 form.
+inline uint32_t hostemu_raw_buffer_load_b32(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff, int aux) {
+    (void)aux;
+    const uint64_t off = (uint64_t)voff + soff;
+    if (off + 4 > r.num_records) hostemu::fail("buffer load beyond num_records");
+    uint32_t v;
+    std::memcpy(&v, r.base + off, 4);
+    return v;
+}
+inline std::array<uint32_t, 2> hostemu_raw_buffer_load_b64(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff,
+                                                          int aux) {
+    (void)aux;
+    const uint64_t off = (uint64_t)voff + soff;
+    if (off + 8 > r.num_records) hostemu::fail("buffer load beyond num_records");
+    std::array<uint32_t, 2> v;
+    std::memcpy(v.data(), r.base + off, 8);
+    return v;
+}
 #define __builtin_amdgcn_make_buffer_rsrc hostemu_make_buffer_rsrc
 #define __builtin_amdgcn_raw_buffer_load_b128 hostemu_raw_buffer_load_b128
+#define __builtin_amdgcn_raw_buffer_load_b32 hostemu_raw_buffer_load_b32
+#define __builtin_amdgcn_raw_buffer_load_b64 hostemu_raw_buffer_load_b64
 #define __builtin_amdgcn_raw_buffer_store_b128 hostemu_raw_buffer_store_b128
 
 // Buffer -> LDS load (gfx950 buffer_load_dword{,x4} ... lds), 4 or 16 bytes

@@ -19,7 +19,11 @@ written generically in R, and the R >= 3 cases pin that on the CPU.
 Cases follow the GPU decode tests: configs[0] (local layer, pos 511), a
 ring-wrapped local layer (pos 1500, window 1024), one split and many, QK-norm
 on and off, non-temporal and plain loads, groups 1 / 2 / 4, and the
-gemma3_gqa-shaped path with and without an additive mask.
+gemma3_gqa-shaped path with and without an additive mask.  The one-launch
+form (splits merged in the kernel by the last workgroup of each run to
+arrive) runs with the workgroups in grid order and in reverse, so the last
+split and the first each do the merging, and must leave its arrival
+counters zero.
 """
 import os
 import subprocess
@@ -47,7 +51,7 @@ def built():
 
 def _run(exe, tmp, *, fused, group, n_kv, n_heads, kc, vc, row_stride, head_stride, n_stream, skip,
          new_slot, rps, n_splits, q, k_new=None, v_new=None, norm=None, rope_row=None, mask=None,
-         nt_loads=0, eps=1e-6, qscale=0.0625 * LOG2E):
+         nt_loads=0, eps=1e-6, qscale=0.0625 * LOG2E, xm_heads=0, order=None):
     os.makedirs(tmp, exist_ok=True)
 
     def put(name, a, dtype=np.float32):
@@ -68,8 +72,10 @@ def _run(exe, tmp, *, fused, group, n_kv, n_heads, kc, vc, row_stride, head_stri
     with open(os.path.join(tmp, "args.txt"), "w") as f:
         f.write(f"{int(fused)} {group} {n_kv} {n_heads} {kc.size} {row_stride} {head_stride} {n_stream} "
                 f"{skip} {new_slot} {rps} {n_splits} {nt_loads} {int(norm is not None)} "
-                f"{int(mask is not None)} {float(np.float32(eps))!r} {float(np.float32(qscale))!r}\n")
+                f"{int(mask is not None)} {float(np.float32(eps))!r} {float(np.float32(qscale))!r} {xm_heads}\n")
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="print_stacktrace=1")
+    if order:
+        env["HOSTEMU_WG_ORDER"] = order
     r = subprocess.run([os.path.join(BUILD, exe), tmp], capture_output=True, text=True, timeout=600, env=env)
     assert r.returncode == 0 and "decode_emu: ok" in r.stdout, (exe, r.stderr[-4000:])
     assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, r.stderr[-4000:]
@@ -80,7 +86,7 @@ def _run(exe, tmp, *, fused, group, n_kv, n_heads, kc, vc, row_stride, head_stri
     return get("out", n_heads * D), get("kc_out", kc.size), get("vc_out", vc.size)
 
 
-def _fused(exe, tmp, case: DecodeCase, rps, n_splits, nt_loads):
+def _fused(exe, tmp, case: DecodeCase, rps, n_splits, nt_loads, xm_heads=0, order=None):
     """g3k_decode as g3attn_decode_device sets it up (host/g3attn.c), over a
     head-major cache holding the case's history; checks the output and the
     new token's cache rows against the oracle."""
@@ -95,7 +101,7 @@ def _fused(exe, tmp, case: DecodeCase, rps, n_splits, nt_loads):
                        kc=hm(Kc), vc=hm(Vc), row_stride=D, head_stride=case.rows * D, n_stream=seq_len - 1,
                        skip=slot, new_slot=slot, rps=rps, n_splits=n_splits, q=case.q, k_new=case.k,
                        v_new=case.v, norm=case.norm, rope_row=case.table.reshape(-1, D)[pos],
-                       nt_loads=nt_loads)
+                       nt_loads=nt_loads, xm_heads=xm_heads, order=order)
     kc = kc.reshape(n_kv, case.rows, D)
     vc = vc.reshape(n_kv, case.rows, D)
     # the new token's rows: k normed + rotated (fp32 rounding may differ), v as given
@@ -169,4 +175,25 @@ def test_gqa_shaped(built, tmp_path, exe, masked):
     assert np.array_equal(kc, k) and np.array_equal(vc, v)
     err = rel_err(got, want)
     print(f"[hostemu {exe}] gqa masked={masked} rel_err={err:.3e}")
+    assert err < BAR
+
+
+@pytest.mark.parametrize("order", ["forward", "reverse"])
+@pytest.mark.parametrize("n_heads,n_kv,xm,pos,layer,rps", [
+    (8, 4, 1, 511, 0, 32),     # configs[0]: 16 splits, one query head per workgroup (8 runs)
+    (8, 4, 1, 1500, 2, 32),    # ring-wrapped local layer: 32 splits of 32 rows
+    (8, 4, 1, 300, 5, 64),     # a global layer, 5 splits of 64 rows
+    (8, 4, 2, 1500, 2, 32),    # whole groups: 4 runs padded to 8 (idle workgroups)
+    (16, 8, 2, 700, 1, 32),    # group 2 over 8 KV heads: whole groups per workgroup
+    (8, 8, 1, 200, 3, 32),     # group 1
+    (8, 2, 1, 400, 4, 32),     # group 4, one query head per workgroup
+])
+def test_one_launch_merge(built, tmp_path, order, n_heads, n_kv, xm, pos, layer, rps):
+    """The one-launch form (xm_heads > 0) against the oracle, with the
+    workgroups in grid order and in reverse."""
+    case = DecodeCase(1, layer=layer, pos=pos, max_context=2048, n_heads=n_heads, n_kv=n_kv)
+    n_stream = (pos + 1 if (case.is_global or pos < 1024) else 1024) - 1
+    err = _fused("decode_emu", str(tmp_path), case, *_splits(n_stream, rps), nt_loads=int(case.is_global),
+                 xm_heads=xm, order=order)
+    print(f"[hostemu xm {order}] H_q {n_heads} H_kv {n_kv} pos {pos} rel_err={err:.3e}")
     assert err < BAR

@@ -149,6 +149,39 @@ def test_load_forms_agree(monkeypatch):
                 assert np.array_equal(a, b), (n_heads, n_kv, mode)
 
 
+def test_one_launch_merge(monkeypatch):
+    """Splits merged inside the decode kernel, on each run's XCD, by the last
+    workgroup to arrive (the default for local layers wherever the placement
+    probe at create passes, as on MI355X), against the two-launch form
+    (G3ATTN_DECODE_XMERGE=0) and the oracle: configs[0]'s 16 splits, full
+    rings of 32 splits, a short global layer admitted by
+    G3ATTN_DECODE_XMERGE=2 (10 splits), each decoded twice on one context
+    (the arrival counters are back at zero after every launch), groups 2 and
+    4.  The forms differ only in the order of the split merge: fp32 sums of
+    up to 32 weighted partials, a few ulp apart (1.2e-6 x RMS seen; bar
+    1e-5, against the decode's 1e-4)."""
+    for n_heads, n_kv in ((8, 4), (8, 2)):
+        outs = {}
+        for mode in ("0", "1", "2"):
+            monkeypatch.setenv("G3ATTN_DECODE_XMERGE", mode)
+            ctx = _ctx(4096, num_layers=6, n_heads=n_heads, n_kv=n_kv)
+            try:
+                got = []
+                for layer, pos in ((0, 511), (1, 2500), (2, 4095), (5, 300)):
+                    case = DecodeCase(16, layer=layer, pos=pos, max_context=4096, n_heads=n_heads, n_kv=n_kv)
+                    _check(case, ctx, f"xm{mode}")
+                    one_launch = mode == "2" or (mode == "1" and not case.is_global)
+                    assert ctx.last_splits(2) == (1 if one_launch else 0), (mode, layer)
+                    assert ctx.last_splits(0) > 1
+                    got.append(case.gpu(ctx))   # again: the counters were left at zero
+                outs[mode] = got
+            finally:
+                ctx.close()
+        for mode in ("1", "2"):
+            for a, b in zip(outs["0"], outs[mode]):
+                assert rel_err(b, a) < 1e-5, (n_heads, n_kv, mode)
+
+
 @pytest.mark.parametrize("env", [{"G3ATTN_SPLIT_ROWS": "1000000"}, {"G3ATTN_SPLIT_ROWS": "32"},
                                  {"G3ATTN_SPLIT_ROWS": "100"}, {"G3ATTN_DECODE_WGS": "8"},
                                  {"G3ATTN_DECODE_WGS": "4000"}, {"G3ATTN_SPLIT_MIN_ROWS": "512"}])

@@ -61,7 +61,9 @@ typedef struct {
 /* One-launch decode: at most this many splits, and the arrival counters,
  * one per (KV head, query-head run) and G3K_XM_COUNTER_STRIDE apart (their
  * own 256-byte line each), in a zeroed buffer that every launch leaves zero. */
+#ifndef G3K_XM_MAX_SPLITS
 #define G3K_XM_MAX_SPLITS 32
+#endif
 #define G3K_XM_COUNTER_STRIDE 64
 #define G3K_XM_COUNTERS(n_heads) ((size_t)(n_heads) * G3K_XM_COUNTER_STRIDE)
 

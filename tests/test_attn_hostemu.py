@@ -563,3 +563,28 @@ def test_front_launch_with_an_empty_batch(built, tmp_path):
     want = np.zeros((hkv, D, ldk), np.uint16)
     want[:, :, :nk] = bits.transpose(1, 2, 0)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("order", ["forward", "reverse"])
+def test_one_launch_local_decode(built, tmp_path, order):
+    """Local-layer decodes at 8 query / 4 KV heads over 95 cached rows (three
+    32-row splits) take the one-launch form: the placement probe at create
+    passes on the emulated machine (workgroup i on XCD i mod 8), so each
+    query head's splits are merged in the kernel by the last to arrive and
+    no combine launch follows.  With G3ATTN_DECODE_XMERGE=0 the same script
+    runs as decode + combine.  Both against the oracle, over a ring past its
+    window, with the workgroups in grid order and in reverse."""
+    for xm in (1, 0):
+        d = tmp_path / f"xm{xm}"
+        d.mkdir()
+        e = Emu(d, H=8, Hkv=4, max_context=256, window=96)
+        e.prefill(0, 0, 150)
+        for pos in (150, 151, 152):
+            e.decode(0, pos)
+        e.check_cache(0, 0, 96)
+        env = {"G3ATTN_DECODE_XMERGE": xm}
+        if order == "reverse":
+            env["HOSTEMU_WG_ORDER"] = "reverse"
+        launches = e.run(**env)
+        assert launches["decode_kernel"][0] == 3, launches
+        assert ("combine_kernel" in launches) == (xm == 0), launches

@@ -157,10 +157,11 @@ def test_one_launch_merge(monkeypatch):
     rings of 32 splits, a short global layer admitted by
     G3ATTN_DECODE_XMERGE=2 (10 splits), each decoded twice on one context
     (the arrival counters are back at zero after every launch), groups 2 and
-    4.  The forms differ only in the order of the split merge: fp32 sums of
+    4, and group 2 over 8 KV heads (whole groups per workgroup).  The forms
+    differ only in the order of the split merge: fp32 sums of
     up to 32 weighted partials, a few ulp apart (1.2e-6 x RMS seen; bar
     1e-5, against the decode's 1e-4)."""
-    for n_heads, n_kv in ((8, 4), (8, 2)):
+    for n_heads, n_kv in ((8, 4), (8, 2), (16, 8)):
         outs = {}
         for mode in ("0", "1", "2"):
             monkeypatch.setenv("G3ATTN_DECODE_XMERGE", mode)
@@ -171,7 +172,8 @@ def test_one_launch_merge(monkeypatch):
                     case = DecodeCase(16, layer=layer, pos=pos, max_context=4096, n_heads=n_heads, n_kv=n_kv)
                     _check(case, ctx, f"xm{mode}")
                     one_launch = mode == "2" or (mode == "1" and not case.is_global)
-                    assert ctx.last_splits(2) == (1 if one_launch else 0), (mode, layer)
+                    heads_per_wg = 2 if n_kv == 8 else 1
+                    assert ctx.last_splits(2) == (heads_per_wg if one_launch else 0), (mode, layer)
                     assert ctx.last_splits(0) > 1
                     got.append(case.gpu(ctx))   # again: the counters were left at zero
                 outs[mode] = got

@@ -443,6 +443,9 @@ def main():
             "kernel_us": round(ks * 1e6, 2),
             "GB/s": round(decode_bytes(512) / (region / 200) / 1e9, 1),
             "bytes_per_call": decode_bytes(512),
+            # one launch: the splits merged in one XCD's L2 (kernel_us then
+            # covers the merge); else decode_kernel + combine_kernel
+            "form": "one launch" if ctx.last_splits(2) else "decode + combine",
         }
         log(f"[bench] local512: {extra['decode_local_L512']}")
         ctx.close()
@@ -474,6 +477,8 @@ def main():
         }
         log(f"[bench] 128k: {extra['decode_global_L131072']}")
         # 34-layer stack: one token through every layer's attention
+        B.decode_calls([(ctx, locs[0])], pos, qkv, zn, out)[0]()
+        local_form = "one launch" if ctx.last_splits(2) else "decode + combine"
         for name, layers in (("reference_29local_5global", list(range(34))),
                              ("literal_28local_6global", glob + locs[:28])):
             layers = sorted(layers)
@@ -490,6 +495,7 @@ def main():
                 "GB/s": round(byts / (region / 20) / 1e9, 1),
                 "frac_of_hbm_peak": round(byts / (region / 20) / 1e9 / HBM_PEAK_GBS, 4),
                 "bytes_per_token": byts,
+                "local_layer_form": local_form,
             }
             log(f"[bench] stack {name}: {extra[f'decode_stack34_L131072_{name}']}")
         ctx.close()

@@ -37,6 +37,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <pthread.h>
+#include <type_traits>
 
 #include "g3k.h"
 #include "g3k_device.h"
@@ -521,85 +522,61 @@ __global__ __launch_bounds__(NT, 2) void decode_kernel(g3k_decode_args p) {
 }
 
 // Cross-split combine, one launch after decode_kernel (kernel order makes
-// the partials visible; no fences or atomics).  grid (D / 32, group, H_kv),
-// 256 threads: lane f = t % 8 owns dims 32 x + 4 f .. + 3, split lane
-// t / 8 takes splits t / 8 + 32 u.  Every partial a thread needs is loaded
-// at once (one memory round trip), merged in registers, then across the 8
-// split lanes of a wave by shuffles and across the 4 waves through LDS.
-constexpr int CMB_SL = NT / 8;                     // split lanes per workgroup
-constexpr int CMB_U = G3K_MAX_SPLITS / CMB_SL;     // splits per thread, at most
-
+// the partials visible; no fences or atomics).  Each wave owns 4 dims of one
+// query head and merges every split across its 64 lanes: lane l loads the
+// partials of splits l, l + 64, ... at once (one memory round trip) and
+// merges them in registers; the lanes then meet pairwise, l ^ 1 and l ^ 2
+// (DPP quad_perm), the quads and the half-rows of a 16-lane row (DPP
+// row_half_mirror, row_mirror), and the rows (v_permlane16/32_swap), all VALU:
+// no LDS and no barrier.  grid (D / 16, group, H_kv), 4 waves per
+// workgroup.  (A workgroup-wide form, 8 split lanes per wave and the 4 waves
+// merged through LDS, took 0.55 us more per 8K decode step.)
 template <int G>
 __global__ __launch_bounds__(NT) void combine_kernel(g3k_decode_args p) {
-    const int x = blockIdx.x, g = blockIdx.y, kvh = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int f = tid & 7, sl = tid >> 3;
-    const int d = 32 * x + 4 * f;
+    const int g = blockIdx.y, kvh = blockIdx.z;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int d = 4 * (blockIdx.x * NW + wave);
     const int S = p.n_splits;
     const size_t slot0 = (size_t)kvh * G3K_MAX_SPLITS;
-    float mq[CMB_U], lq[CMB_U];
-    float4 aq[CMB_U];
+    constexpr int U = G3K_MAX_SPLITS / 64;   // splits per lane, at most
+    float2 mlq[U];
+    float4 aq[U];
 #pragma unroll
-    for (int u = 0; u < CMB_U; u++) {
-        const int q = sl + CMB_SL * u;
-        if (q < S) {
-            const size_t sg = (slot0 + q) * G + g;
-            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + sg * 2);
-            mq[u] = ml.x;
-            lq[u] = ml.y;
+    for (int u = 0; u < U; u++) {
+        const int s = lane + 64 * u;
+        if (s < S) {
+            const size_t sg = (slot0 + s) * G + g;
+            mlq[u] = *reinterpret_cast<const float2 *>(p.ws_ml + sg * 2);
             aq[u] = *reinterpret_cast<const float4 *>(p.ws_acc + sg * D + d);
         } else {
-            mq[u] = NEG_BIG;
-            lq[u] = 0.f;
+            mlq[u] = make_float2(NEG_BIG, 0.f);
             aq[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
-    float M = NEG_BIG;
-#pragma unroll
-    for (int u = 0; u < CMB_U; u++) M = fmaxf(M, mq[u]);
-    float L = 0.f;
+    float M = NEG_BIG, L = 0.f;
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int u = 0; u < CMB_U; u++) {
-        const float b = fast_exp2(mq[u] - M);
-        L += lq[u] * b;
-        A.x += aq[u].x * b;
-        A.y += aq[u].y * b;
-        A.z += aq[u].z * b;
-        A.w += aq[u].w * b;
-    }
-    // the 8 split lanes of this wave: lanes f + 8 k.  Lanes l and l ^ 8 meet
-    // through DPP row_ror:8 (l ^ 8 within a 16-lane row), then l ^ 16 and
-    // l ^ 32 through v_permlane16/32_swap, whose two results hold the lower
-    // lane's partial, then the upper lane's, in both lanes: all VALU, no LDS
-    // round trip.  Lanes 0..7 (the ones stored below) merge (own, partner)
-    // at every level.
-    {
+    for (int u = 0; u < U; u++) merge_ml(M, L, A, mlq[u].x, mlq[u].y, aq[u]);
+    auto dpp_merge = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
         float4 a2;
-        const float m2 = dpp<0x128>(M), l2 = dpp<0x128>(L);
-        a2.x = dpp<0x128>(A.x);
-        a2.y = dpp<0x128>(A.y);
-        a2.z = dpp<0x128>(A.z);
-        a2.w = dpp<0x128>(A.w);
+        const float m2 = dpp<C>(M), l2 = dpp<C>(L);
+        a2.x = dpp<C>(A.x);
+        a2.y = dpp<C>(A.y);
+        a2.z = dpp<C>(A.z);
+        a2.w = dpp<C>(A.w);
         merge_ml(M, L, A, m2, l2, a2);
-    }
+    };
+    dpp_merge(std::integral_constant<int, 0xB1>{});    // quad_perm [1,0,3,2]
+    dpp_merge(std::integral_constant<int, 0x4E>{});    // quad_perm [2,3,0,1]
+    dpp_merge(std::integral_constant<int, 0x141>{});   // row_half_mirror
+    dpp_merge(std::integral_constant<int, 0x140>{});   // row_mirror
     swap_merge<16>(M, L, A);
     swap_merge<32>(M, L, A);
-    __shared__ float s_m[NW][8], s_l[NW][8];
-    __shared__ float4 s_a[NW][8];
-    if (lane < 8) {
-        s_m[wave][lane] = M;
-        s_l[wave][lane] = L;
-        s_a[wave][lane] = A;
-    }
-    __syncthreads();
-    if (tid < 8) {
-#pragma unroll
-        for (int w = 1; w < NW; w++) merge_ml(M, L, A, s_m[w][tid], s_l[w][tid], s_a[w][tid]);
-        // a division, as the single-split path's store: one split gives the same bits either way
+    // a division, as the single-split path's store: one split gives the same bits either way
+    if (lane == 0)
         *reinterpret_cast<float4 *>(p.out + ((size_t)kvh * G + g) * D + d) =
             make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
-    }
 }
 
 template <int G, bool FUSED, bool NTL>
@@ -610,7 +587,7 @@ hipError_t launch(const g3k_decode_args *a, hipStream_t st) {
                           (hipEvent_t)a->ev1, 0, *a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a->n_splits == 1) return e;
-    hipLaunchKernelGGL((combine_kernel<G>), dim3(D / 32, G, a->n_kv_heads), dim3(NT), 0, st, *a);
+    hipLaunchKernelGGL((combine_kernel<G>), dim3(D / (4 * NW), G, a->n_kv_heads), dim3(NT), 0, st, *a);
     return hipGetLastError();
 }
 
